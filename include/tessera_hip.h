@@ -1,0 +1,199 @@
+/*
+ * libtessera_hip: gfx950 (MI355X) kernels for tessera's matmul and attention
+ * hot path, behind a plain C ABI.
+ *
+ * Conventions (all entry points):
+ *  - Every pointer is a device pointer unless stated; the caller owns all
+ *    memory. No entry point allocates, frees, copies to/from the host or
+ *    synchronizes: each only enqueues kernels on `stream` (a hipStream_t, NULL
+ *    for the null stream), so every call may be captured into a HIP graph.
+ *  - Scratch (split-K / split-KV partials) comes from a caller-owned
+ *    `workspace` of at least the bytes the matching *_workspace() call reports.
+ *    Its first 256 KiB hold completion counters that must be zero before first
+ *    use; every kernel returns the counters it used to zero, so one workspace,
+ *    zeroed once, serves any sequence of stream-ordered calls. Calls that run
+ *    concurrently (different streams) need separate workspaces.
+ *  - Return 0 on success; a positive value is a passed-through hipError_t; a
+ *    negative value is an argument error (TS_ERR_*). The message for the last
+ *    failure on the calling thread is tessera_hip_last_error(). Nothing aborts.
+ *  - Argument order inside each struct follows the reference Launch order:
+ *    the step's reads, epilogue operands, the output, then the u32 counts.
+ */
+#ifndef TESSERA_HIP_H
+#define TESSERA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TS_OK 0
+#define TS_ERR_ARG (-1)       /* unsupported shape, dtype, alignment or null pointer */
+#define TS_ERR_ARCH (-2)      /* the current device is not gfx950 */
+#define TS_ERR_WORKSPACE (-3) /* workspace missing or too small */
+
+/* Storage types (engine/ir/mem/src/form.rs forms used on this path). */
+enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3 };
+
+/* Fused stages around a product (engine/plan/lower/src/kernels/map.rs:20-59 MapStage,
+ * applied by `finish` at the store, map.rs:155-185). */
+#define TS_AFTER_ADD 1u       /* out = sum + a0[m, n] (the residual add; a0 may alias out) */
+#define TS_AFTER_SILU_MUL 2u  /* w holds 2n rows, gate rows then up rows; out = silu(g) * u */
+#define TS_BEFORE_RMS_NORM 4u /* x rows pass through RmsNorm with `gain` before the product */
+
+/* Version of this ABI; bumped on any struct layout change. */
+#define TS_ABI_VERSION 1
+
+/* Checks that the current device is gfx950 and records its properties.
+ * Replaces: the platform probe of engine/gpu/gpukit/src/rocm/context.rs:60-106
+ * (arch, lanes, group bytes). */
+int tessera_hip_init(void);
+
+/* Thread-local text of the last failure.
+ * Replaces: Runtime::check's error text, engine/gpu/gpukit/src/rocm/hip.rs:98-106. */
+const char *tessera_hip_last_error(void);
+
+int tessera_hip_abi_version(void);
+
+/* ----------------------------------------------------------------------------
+ * Linear: out[m, n] = after(sum_k before(x)[m, k] * w[n, k])
+ * x: [m, k] f32 or bf16 (f32 is split into two exact bf16 parts on the matrix
+ * unit, as the reference's tiled_parts splits f32 rows into bf16 slabs).
+ * w: [n, k] bf16, or e4m3 with a bf16 scale per output row (w_scale [n]).
+ * out: [m, n] f32 or bf16.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void *x;        /* [m, k] */
+    const void *w;        /* [n, k], or [2n, k] with TS_AFTER_SILU_MUL */
+    const void *w_scale;  /* [n] (or [2n]) bf16, e4m3 weights only */
+    const float *gain;    /* [k] f32, TS_BEFORE_RMS_NORM only */
+    const float *a0;      /* [m, n] f32, TS_AFTER_ADD only; may alias out */
+    void *out;            /* [m, n] */
+    void *workspace;
+    size_t workspace_bytes;
+    uint32_t m, n, k;
+    int32_t x_dtype, w_dtype, out_dtype;
+    uint32_t stages;      /* TS_AFTER_* | TS_BEFORE_* bits */
+    float eps;            /* RmsNorm epsilon */
+} ts_linear_args;
+
+/* Picks `lanes` for m <= 16 and `tiled` otherwise (the cost select of
+ * engine/plan/lower/src/cost.rs between the two rules). */
+int tessera_hip_linear(const ts_linear_args *a, void *stream);
+size_t tessera_hip_linear_workspace(const ts_linear_args *a);
+
+/* Few rows (m <= 16): a wave per 16 output columns on the matrix unit, weights
+ * streamed once with 64-byte runs per lane, split-K across waves and groups.
+ * Replaces: rule "lanes" (engine/rules/linear/src/lanes.rs:17-143) and "thin"
+ * (engine/rules/linear/src/thin.rs:11-104). */
+int tessera_hip_lanes(const ts_linear_args *a, void *stream);
+size_t tessera_hip_lanes_workspace(const ts_linear_args *a);
+
+/* Many rows: LDS-staged, double-buffered MFMA tiles.
+ * Replaces: rule "tiled" (engine/rules/linear/src/tiled.rs:281-345,441-453,611-672)
+ * including tiled_parts (tiled.rs:43-49,186-278). */
+int tessera_hip_tiled(const ts_linear_args *a, void *stream);
+
+/* ----------------------------------------------------------------------------
+ * Ragged-row attention over kept (paged) K/V.
+ * Row r (slot s, position p) attends keys [max(0, p - back), p] of slot s; the
+ * key at position j lives at kept row table[s*kept_pages + (j >> log2 page)]
+ * * page + (j & (page-1)) (engine/plan/codegen/src/kept.rs:181-193), or at
+ * s*keys + j when kept_table is NULL. Scores are dot(q, k) * scale.
+ * q: [rows, heads, width] f32; K/V rows: [*, kv_heads, width] bf16;
+ * out: [rows, heads, width] f32. Head h reads kv head h / (heads / kv_heads).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void *q;
+    const void *k;
+    const void *v;
+    void *out;
+    const uint32_t *slots;      /* [rows] */
+    const uint32_t *positions;  /* [rows] */
+    const uint32_t *kept_table; /* [slot count * kept_pages], or NULL for dense */
+    void *workspace;
+    size_t workspace_bytes;
+    uint32_t rows;              /* queries */
+    uint32_t keys;              /* positions a slot may hold (the kept context) */
+    uint32_t heads, kv_heads;
+    uint32_t width;             /* head dim: 128 */
+    uint32_t back;              /* keys a row sees before its own; UINT32_MAX = causal */
+    uint32_t kept_pages;        /* table entries per slot */
+    uint32_t page;              /* rows per page (power of two, >= 16) */
+    float scale;
+    int32_t q_dtype, kv_dtype, out_dtype;
+    uint32_t max_position;      /* an upper bound on positions[] (sizes the split) */
+} ts_rows_args;
+
+/* Decode: few rows, each key range split across workgroups, partial
+ * (max, sum, acc) merged by the last group to finish.
+ * Replaces: rule "attend" / attend_rows (engine/rules/attention/src/attend.rs:126-270)
+ * and flash_rows for decode rows (flash.rs:506-591). */
+int tessera_hip_attend_rows(const ts_rows_args *a, void *stream);
+size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
+
+/* Prefill: 64-row query blocks of one slot on the matrix unit, keys streamed
+ * page by page with online softmax.
+ * Replaces: rule "flash" / flash_rows (engine/rules/attention/src/flash.rs:416-503,
+ * 506-591, 595-807). Rows must come in runs of one slot at consecutive positions
+ * (the prefill shape); each 64-row block must not cross a slot. */
+int tessera_hip_flash_rows(const ts_rows_args *a, void *stream);
+
+/* ----------------------------------------------------------------------------
+ * Row stages and indices.
+ * ------------------------------------------------------------------------- */
+
+/* out = x * rsqrt(mean(x^2) + eps) * gain, per row of `width`; x/out f32.
+ * Replaces: "rms_norm" / "lane_norm" (engine/rules/kernels/src/rms_norm.rs:9-69,
+ * lane_norm.rs:10-96). out may alias x. */
+int tessera_hip_rms_norm(const float *x, const float *gain, float *out, uint32_t rows,
+                         uint32_t width, float eps, void *stream);
+
+/* Rotates (j, j + width/2) pairs (Halves) or (2j, 2j+1) (Adjacent) of each
+ * [rows, heads, width] row in place by angle pos * theta^(-2j/width).
+ * Replaces: "angles" + "rope" (engine/rules/kernels/src/rope.rs:10-125). */
+int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t rows, uint32_t heads,
+                     uint32_t width, float theta, int32_t halves, void *stream);
+
+/* The step between the q/k/v product and attention for a Qwen3 layer: per head
+ * RmsNorm (q_gain / k_gain, eps) then Halves RoPE on q and k, then the new k
+ * and v rows written (bf16) into the kept rows at (slot, position).
+ * qkv: [rows, (heads + 2*kv_heads) * width] f32 (q heads, then k, then v).
+ * q_out: [rows, heads, width] f32.
+ * Replaces: the q_norm/k_norm RmsNorm + rope + Append chain
+ * (engine/models/src/shared.rs:109-145, engine/ir/interp/src/run.rs:122-198). */
+int tessera_hip_qk_norm_rope_append(const float *qkv, const float *q_gain, const float *k_gain,
+                                    float *q_out, void *k_cache, void *v_cache,
+                                    const uint32_t *slots, const uint32_t *positions,
+                                    const uint32_t *kept_table, uint32_t rows, uint32_t heads,
+                                    uint32_t kv_heads, uint32_t width, uint32_t keys,
+                                    uint32_t kept_pages, uint32_t page, float eps, float theta,
+                                    void *stream);
+
+/* Embedding rows: out[r, :] = f32(table[ids[r] - first, :]), zeros outside the
+ * table. table bf16 [rows_in_table, width].
+ * Replaces: "gather" (engine/rules/kernels/src/gather.rs; interp cpu.rs:511-525). */
+int tessera_hip_gather(const void *table, const uint32_t *ids, float *out, uint32_t count,
+                       uint32_t table_rows, uint32_t width, uint32_t first, void *stream);
+
+/* ids[r] = first index of the largest finite entry of row r (NaN and -inf
+ * skipped; `width` when none). x f32 [rows, width].
+ * Replaces: "peaks" + "argmax" (engine/rules/kernels/src/argmax.rs:74-129). */
+int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, uint32_t width,
+                       void *workspace, size_t workspace_bytes, void *stream);
+size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width);
+
+/* ids[r, 0..k): the row's k largest finite entries, best first, ties to the
+ * lower index, NaN/-inf skipped, spare slots = width. x f32 [rows, width],
+ * width <= 1024, k <= 32.
+ * Replaces: "top_k" (engine/rules/kernels/src/argmax.rs:39-72; interp run.rs:577-591). */
+int tessera_hip_top_k(const float *x, uint32_t *ids, uint32_t rows, uint32_t width, uint32_t k,
+                      void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TESSERA_HIP_H */

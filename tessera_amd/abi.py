@@ -1,0 +1,132 @@
+"""ctypes binding of libtessera_hip.so: the C ABI declared in include/tessera_hip.h.
+
+This plays the part of the reference's ``tessera_dl::library!`` struct
+(engine/gpu/dl/src/lib.rs:66) that engine/gpu/gpukit/src/rocm/hip.rs:48-94 uses to
+bind libamdhip64: one table of typed function pointers, resolved once. Loading fails
+loudly when the library has not been built; there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtessera_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "tessera_hip.h")
+
+TS_OK = 0
+TS_ERR_ARG = -1
+TS_ERR_ARCH = -2
+TS_ERR_WORKSPACE = -3
+
+TS_F32, TS_BF16, TS_E4M3, TS_U32 = 0, 1, 2, 3
+
+TS_AFTER_ADD = 1
+TS_AFTER_SILU_MUL = 2
+TS_BEFORE_RMS_NORM = 4
+
+U32_MAX = 0xFFFFFFFF
+
+
+class LinearArgs(C.Structure):
+    """ts_linear_args (include/tessera_hip.h)."""
+    _fields_ = [
+        ("x", C.c_void_p), ("w", C.c_void_p), ("w_scale", C.c_void_p), ("gain", C.c_void_p),
+        ("a0", C.c_void_p), ("out", C.c_void_p), ("workspace", C.c_void_p),
+        ("workspace_bytes", C.c_size_t),
+        ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32),
+        ("x_dtype", C.c_int32), ("w_dtype", C.c_int32), ("out_dtype", C.c_int32),
+        ("stages", C.c_uint32), ("eps", C.c_float),
+    ]
+
+
+class RowsArgs(C.Structure):
+    """ts_rows_args (include/tessera_hip.h)."""
+    _fields_ = [
+        ("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("out", C.c_void_p),
+        ("slots", C.c_void_p), ("positions", C.c_void_p), ("kept_table", C.c_void_p),
+        ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("rows", C.c_uint32), ("keys", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32),
+        ("width", C.c_uint32), ("back", C.c_uint32), ("kept_pages", C.c_uint32), ("page", C.c_uint32),
+        ("scale", C.c_float), ("q_dtype", C.c_int32), ("kv_dtype", C.c_int32), ("out_dtype", C.c_int32),
+        ("max_position", C.c_uint32),
+    ]
+
+
+_P = C.c_void_p
+_U = C.c_uint32
+_LA = C.POINTER(LinearArgs)
+_RA = C.POINTER(RowsArgs)
+
+SIGNATURES = {
+    "tessera_hip_init": (C.c_int, []),
+    "tessera_hip_last_error": (C.c_char_p, []),
+    "tessera_hip_abi_version": (C.c_int, []),
+    "tessera_hip_linear": (C.c_int, [_LA, _P]),
+    "tessera_hip_linear_workspace": (C.c_size_t, [_LA]),
+    "tessera_hip_lanes": (C.c_int, [_LA, _P]),
+    "tessera_hip_lanes_workspace": (C.c_size_t, [_LA]),
+    "tessera_hip_tiled": (C.c_int, [_LA, _P]),
+    "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
+    "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
+    "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),
+    "tessera_hip_rms_norm": (C.c_int, [_P, _P, _P, _U, _U, C.c_float, _P]),
+    "tessera_hip_rope": (C.c_int, [_P, _P, _U, _U, _U, C.c_float, C.c_int32, _P]),
+    "tessera_hip_qk_norm_rope_append": (C.c_int, [_P] * 9 + [_U] * 7 + [C.c_float, C.c_float, _P]),
+    "tessera_hip_gather": (C.c_int, [_P, _P, _P, _U, _U, _U, _U, _P]),
+    "tessera_hip_argmax": (C.c_int, [_P, _P, _U, _U, _P, C.c_size_t, _P]),
+    "tessera_hip_argmax_workspace": (C.c_size_t, [_U, _U]),
+    "tessera_hip_top_k": (C.c_int, [_P, _P, _U, _U, _U, _P]),
+}
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, what: str, message: str):
+        super().__init__(f"{what} returned {code}: {message}")
+        self.code = code
+
+
+_lib = None
+
+
+def load():
+    """The resolved library. Raises if it is missing: there is no CPU fallback."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def declared_functions() -> list[str]:
+    """Every function the public header declares (checked against the exports)."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tessera_hip_\w+)\s*\(", text)))
+
+
+def declared_arity() -> dict[str, int]:
+    """Parameter count of each prototype in the public header."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(tessera_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def check(code: int, what: str) -> None:
+    if code != TS_OK:
+        raise HipError(code, what, load().tessera_hip_last_error().decode())
+
+
+def call(name: str, *args) -> None:
+    check(getattr(load(), name)(*args), name)

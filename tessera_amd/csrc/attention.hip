@@ -1,0 +1,299 @@
+// Ragged-row attention over kept (paged) K/V: the decode kernel.
+//
+// Replaces the reference's attend_rows rule (one 256-thread group per
+// (row, head), a block reduction per key: engine/rules/attention/src/attend.rs:
+// 126-270) and flash_rows for decode rows (flash.rs:506-591). Semantics follow
+// the interpreter: keys [max(0, pos - back), pos] of the row's slot, scores
+// dot(q, k) * scale, softmax, sum of p * v (engine/ir/interp/src/cpu.rs:
+// 141-167, 293-351). Kept rows are addressed through the page table as
+// engine/plan/codegen/src/kept.rs:181-193 does.
+//
+// gfx950 design (HBM-bound: every K/V byte read once):
+//  * One group per (row, kv head, key partition): all G = heads/kv_heads query
+//    heads that share the kv head ride along, so K/V are read once per GQA group.
+//  * Keys go 16 at a time (one page-aligned block; pages hold >= 16 rows so a
+//    block is one table lookup). Scores S[16 heads, 16 keys] come from four
+//    v_mfma_f32_16x16x32_bf16 steps per q part: each lane loads 64 contiguous
+//    bytes of one key row (B operand), q is split into two bf16 parts.
+//  * Online softmax per head in registers (16-lane butterflies), then P*V on
+//    the vector ALUs: a lane owns 2 adjacent head dims, so each V row is one
+//    256-byte coalesced load across the wave.
+//  * Partitions are merged (max, sum, acc) in LDS across the group's 4 waves and
+//    in the workspace across groups, the last group to finish combining them in
+//    partition order.
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kMaxG = 16;
+
+struct RowsParams {
+    const float *q;
+    const uint16_t *k, *v;
+    float *out;
+    const uint32_t *slots, *positions, *table;
+    float *partials;     // [rows][kv_heads][parts][G][2 + 128]
+    uint32_t *counters;  // [rows][kv_heads]
+    uint32_t rows, keys, heads, kv_heads, G, back, kept_pages, page_shift;
+    uint32_t wave_keys;  // keys per wave per partition (multiple of 16)
+    float scale;
+};
+
+TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
+    if (!p.table) return (uint64_t)slot * p.keys + pos;
+    const uint64_t entry = (uint64_t)slot * p.kept_pages + (pos >> p.page_shift);
+    return ((uint64_t)p.table[entry] << p.page_shift) | (pos & ((1u << p.page_shift) - 1));
+}
+
+template <int G>
+__global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z, parts = gridDim.x;
+    const uint32_t col = lane & 15, grp = lane >> 4;
+
+    __shared__ float sp[kWaves][16][G];  // p[key][head] of the current block
+    __shared__ float salpha[kWaves][G];
+    __shared__ float sm[kWaves][G], sl[kWaves][G];
+    __shared__ float so[kWaves][G][128];
+    __shared__ uint32_t last_s;
+
+    const uint32_t pos = p.positions[r], slot = p.slots[r];
+    const uint32_t from = pos > p.back ? pos - p.back : 0;
+
+    // q operand: row (head) col of the group, d-group grp; two bf16 parts.
+    u32x4 qh[4], ql[4];
+    {
+        const bool ok = col < G;
+        const float *qr = p.q + ((size_t)r * p.heads + kvh * G + (ok ? col : 0)) * 128 + 32 * grp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float a = ok ? qr[8 * j + 2 * e] : 0.0f, b = ok ? qr[8 * j + 2 * e + 1] : 0.0f;
+                float ha = bf16_round(a), hb = bf16_round(b);
+                h[e] = pack_bf16x2(ha, hb);
+                l[e] = pack_bf16x2(a - ha, b - hb);
+            }
+            qh[j] = u32x4{h[0], h[1], h[2], h[3]};
+            ql[j] = u32x4{l[0], l[1], l[2], l[3]};
+        }
+    }
+
+    // Online softmax state: this lane's 4 head rows (4*grp + i) in the S layout.
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
+    // Accumulator: heads h < G, dims 2*lane, 2*lane+1.
+    float o0[G], o1[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) { o0[h] = 0.0f; o1[h] = 0.0f; }
+
+    const uint32_t wk0 = (part * kWaves + wave) * p.wave_keys;
+    const uint32_t blocks = p.wave_keys / 16;
+    for (uint32_t b = 0; b < blocks; b++) {
+        const uint32_t kb = wk0 + 16 * b;
+        const bool live = kb <= pos && kb + 16 > from;  // uniform across the wave
+        if (live) {
+            const uint64_t row0 = kept_row(p, slot, kb);  // 16 rows of one page
+            const uint32_t key = kb + col;
+            const uint16_t *kr = p.k + ((row0 + col) * p.kv_heads + kvh) * 128 + 32 * grp;
+            // Dense kept rows end at the slot's capacity; pages always hold whole blocks.
+            const bool in_mem = p.table || key < p.keys;
+            u32x4 kk[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) kk[j] = in_mem ? *((const u32x4 *)kr + j) : u32x4{0, 0, 0, 0};
+            f32x4 s = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                s = mfma16(as_bf16x8(qh[j]), as_bf16x8(kk[j]), s);
+                s = mfma16(as_bf16x8(ql[j]), as_bf16x8(kk[j]), s);
+            }
+            const bool valid = key >= from && key <= pos;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float si = valid ? s[i] * p.scale : -INFINITY;
+                float mx = si;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                const float mn = fmaxf(m[i], mx);
+                const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
+                const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
+                float sum = pi;
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
+                l[i] = l[i] * alpha + sum;
+                m[i] = mn;
+                const uint32_t h = 4 * grp + i;
+                if (h < G) {
+                    sp[wave][col][h] = pi;
+                    if (col == 0) salpha[wave][h] = alpha;
+                }
+            }
+        }
+        __syncthreads();
+        if (live) {
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float a = salpha[wave][h];
+                o0[h] *= a;
+                o1[h] *= a;
+            }
+            const uint32_t kmax = min(kb + 16, pos + 1);
+            const uint64_t row0 = kept_row(p, slot, kb);
+            for (uint32_t key = max(kb, from); key < kmax; key++) {
+                const uint32_t i = key - kb;
+                const uint32_t vv = *((const uint32_t *)(p.v + ((row0 + i) * p.kv_heads + kvh) * 128) + lane);
+                const float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
+#pragma unroll
+                for (int h = 0; h < G; h++) {
+                    const float pk = sp[wave][i][h];
+                    o0[h] += pk * v0;
+                    o1[h] += pk * v1;
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // Merge the 4 waves of this group.
+    if (col == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t h = 4 * grp + i;
+            if (h < G) { sm[wave][h] = m[i]; sl[wave][h] = l[i]; }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        so[wave][h][2 * lane] = o0[h];
+        so[wave][h][2 * lane + 1] = o1[h];
+    }
+    __syncthreads();
+
+    const uint32_t t = threadIdx.x;
+    const size_t gi = (size_t)r * p.kv_heads + kvh;
+    float *mine = p.partials ? p.partials + (gi * parts + part) * G * 130 : nullptr;
+    for (uint32_t e = t; e < G * 128; e += blockDim.x) {
+        const uint32_t h = e / 128, d = e % 128;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, sm[w][h]);
+        float L = 0.0f, O = 0.0f;
+        for (int w = 0; w < kWaves; w++) {
+            const float f = (sm[w][h] == -INFINITY) ? 0.0f : expf(sm[w][h] - M);
+            L += sl[w][h] * f;
+            O += so[w][h][d] * f;
+        }
+        if (parts == 1) {
+            p.out[((size_t)r * p.heads + kvh * G + h) * 128 + d] = O / L;
+        } else {
+            mine[h * 130 + 2 + d] = O;
+            if (d == 0) { mine[h * 130] = M; mine[h * 130 + 1] = L; }
+        }
+    }
+    if (parts == 1) return;
+    __threadfence();
+    __syncthreads();
+    if (t == 0) last_s = atomicAdd(&p.counters[gi], 1u) == parts - 1;
+    __syncthreads();
+    if (!last_s) return;
+    __threadfence();
+    const float *all = p.partials + gi * parts * G * 130;
+    for (uint32_t e = t; e < G * 128; e += blockDim.x) {
+        const uint32_t h = e / 128, d = e % 128;
+        float M = -INFINITY;
+        for (uint32_t q = 0; q < parts; q++) M = fmaxf(M, __builtin_nontemporal_load(all + (q * G + h) * 130));
+        float L = 0.0f, O = 0.0f;
+        for (uint32_t q = 0; q < parts; q++) {
+            const float *pq = all + (q * G + h) * 130;
+            const float mq = __builtin_nontemporal_load(pq);
+            const float f = (mq == -INFINITY) ? 0.0f : expf(mq - M);
+            L += __builtin_nontemporal_load(pq + 1) * f;
+            O += __builtin_nontemporal_load(pq + 2 + d) * f;
+        }
+        p.out[((size_t)r * p.heads + kvh * G + h) * 128 + d] = O / L;
+    }
+    if (t == 0) p.counters[gi] = 0;
+}
+
+struct Split {
+    uint32_t wave_keys, parts;
+};
+
+Split split(const ts_rows_args *a) {
+    const uint32_t span = a->max_position + 1;
+    uint32_t wave_keys = 64;
+    if (span <= 1024) wave_keys = 16;
+    else if (span <= 4096) wave_keys = 32;
+    Split s;
+    s.wave_keys = wave_keys;
+    s.parts = (span + kWaves * wave_keys - 1) / (kWaves * wave_keys);
+    return s;
+}
+
+int check(const ts_rows_args *a) {
+    TS_REQUIRE(a && a->q && a->k && a->v && a->out && a->slots && a->positions, "attend_rows: null pointer");
+    TS_REQUIRE(a->width == 128, "attend_rows: head width %u (128 supported)", a->width);
+    TS_REQUIRE(a->kv_heads >= 1 && a->heads % a->kv_heads == 0, "attend_rows: %u heads over %u kv heads",
+               a->heads, a->kv_heads);
+    TS_REQUIRE(a->heads / a->kv_heads <= kMaxG, "attend_rows: %u query heads per kv head (at most %d)",
+               a->heads / a->kv_heads, kMaxG);
+    TS_REQUIRE(a->q_dtype == TS_F32 && a->kv_dtype == TS_BF16 && a->out_dtype == TS_F32,
+               "attend_rows: q f32, kept rows bf16, out f32 supported");
+    TS_REQUIRE(!a->kept_table || (a->page >= 16 && (a->page & (a->page - 1)) == 0),
+               "attend_rows: page %u must be a power of two >= 16", a->page);
+    TS_REQUIRE(a->kept_table || a->keys >= 1, "attend_rows: dense kept rows need keys");
+    TS_REQUIRE(ts::aligned(a->k, 16) && ts::aligned(a->v, 16) && ts::aligned(a->q, 16),
+               "attend_rows: q, k, v must be 16-byte aligned");
+    TS_REQUIRE(a->kv_heads <= 65535 && a->rows <= 65535, "attend_rows: grid limits");
+    return TS_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
+    if (!a || a->kv_heads == 0) return 0;
+    Split s = split(a);
+    if (s.parts <= 1) return 0;
+    const size_t G = a->heads / a->kv_heads;
+    const size_t groups = (size_t)a->rows * a->kv_heads;
+    return kWsScratch + groups * s.parts * G * 130 * sizeof(float);
+}
+
+extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
+    int rc = check(a);
+    if (rc) return rc;
+    if (a->rows == 0) return TS_OK;
+    Split s = split(a);
+    RowsParams p;
+    p.q = (const float *)a->q; p.k = (const uint16_t *)a->k; p.v = (const uint16_t *)a->v;
+    p.out = (float *)a->out; p.slots = a->slots; p.positions = a->positions; p.table = a->kept_table;
+    p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads;
+    p.G = a->heads / a->kv_heads; p.back = a->back; p.kept_pages = a->kept_pages;
+    p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
+    p.wave_keys = s.wave_keys; p.scale = a->scale;
+    p.partials = nullptr; p.counters = nullptr;
+    if (s.parts > 1) {
+        const size_t need = tessera_hip_attend_rows_workspace(a);
+        if (!a->workspace || a->workspace_bytes < need)
+            return ts::fail(TS_ERR_WORKSPACE, "attend_rows: workspace of %zu bytes needed", need);
+        const size_t groups = (size_t)a->rows * a->kv_heads;
+        TS_REQUIRE(groups <= kWsCounters, "attend_rows: %zu row x kv-head groups (at most %zu)", groups,
+                   kWsCounters);
+        p.counters = (uint32_t *)a->workspace;
+        p.partials = (float *)((char *)a->workspace + kWsScratch);
+    }
+    void (*k)(RowsParams) = nullptr;
+    switch (p.G) {
+    case 1: k = attend_rows_kernel<1>; break;
+    case 2: k = attend_rows_kernel<2>; break;
+    case 4: k = attend_rows_kernel<4>; break;
+    case 8: k = attend_rows_kernel<8>; break;
+    case 16: k = attend_rows_kernel<16>; break;
+    default: return ts::fail(TS_ERR_ARG, "attend_rows: %u query heads per kv head (1, 2, 4, 8 or 16)", p.G);
+    }
+    hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+    TS_CHECK_LAUNCH("attend_rows launch");
+    return TS_OK;
+}

@@ -1,0 +1,112 @@
+// Shared device and host helpers for the gfx950 kernels behind libtessera_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/tessera_hip.h"
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define TS_DEV __device__ __forceinline__
+
+// Workspace layout shared by every entry point: counters first (zero at rest:
+// each kernel returns the ones it used to zero), scratch after. Keeping the
+// counters at a fixed place means one workspace serves any sequence of calls.
+constexpr size_t kWsCounters = 65536;
+constexpr size_t kWsScratch = kWsCounters * sizeof(uint32_t);
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing: a thread-local message, an int status code.
+// ---------------------------------------------------------------------------
+namespace ts {
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_status(hipError_t e, const char *what);
+
+#define TS_CHECK_LAUNCH(what)                                             \
+    do {                                                                  \
+        hipError_t _e = hipPeekAtLastError();                             \
+        if (_e != hipSuccess) return ::ts::hip_status(_e, what);          \
+    } while (0)
+
+#define TS_REQUIRE(cond, ...)                                             \
+    do {                                                                  \
+        if (!(cond)) return ::ts::fail(TS_ERR_ARG, __VA_ARGS__);         \
+    } while (0)
+
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace ts
+
+// ---------------------------------------------------------------------------
+// Narrow floats. bf16 narrowing is round-to-nearest-even with NaN kept quiet
+// (the rule of engine/ir/graph/src/scalar.rs:20-44 for 8 exponent and 7
+// mantissa bits; the bit form below gives the same code for every f32,
+// subnormals and overflow to infinity included).
+// ---------------------------------------------------------------------------
+TS_DEV uint16_t bf16_bits(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+TS_DEV float bf16_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+TS_DEV float bf16_round(float x) { return bf16_float(bf16_bits(x)); }
+
+// Two f32 -> packed bf16 pair in one u32 (low half first).
+TS_DEV uint32_t pack_bf16x2(float a, float b) {
+    return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
+}
+
+// Low / high bf16 of a packed u32, as f32 (exact).
+TS_DEV float lo_bf16(uint32_t v) { return __uint_as_float(v << 16); }
+TS_DEV float hi_bf16(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// OCP e4m3 code -> f32. Placing the 7 magnitude bits at f32 bits 20..26 gives
+// 2^(e-127)(1+m/8) for e>0 and the f32 subnormal m/8*2^-126 for e=0; one
+// multiply by 2^120 rebiases both cases exactly. Code 0x7F (NaN) is never
+// produced by the saturating quantizer and is not special-cased here.
+TS_DEV float e4m3_float(uint32_t c) {
+    float mag = __uint_as_float((c & 0x7fu) << 20) * 0x1p120f;
+    return (c & 0x80u) ? -mag : mag;
+}
+
+// Four e4m3 codes (one u32) -> two packed bf16 pairs (exact: 3 mantissa bits).
+TS_DEV u32x2 e4m3x4_to_bf16x4(uint32_t w) {
+    u32x2 r;
+    r.x = pack_bf16x2(e4m3_float(w & 0xff), e4m3_float((w >> 8) & 0xff));
+    r.y = pack_bf16x2(e4m3_float((w >> 16) & 0xff), e4m3_float(w >> 24));
+    return r;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (DPP/permute via the compiler's __shfl_xor).
+// ---------------------------------------------------------------------------
+TS_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+TS_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// MFMA 16x16x32 bf16 -> f32. Operand lane layout (wave64): A lane l holds row
+// l%16, eight k values of the k-group l/16; B lane l holds column l%16 and the
+// same k-group; D lane l holds column l%16, rows 4*(l/16)+0..3.
+TS_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+TS_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }

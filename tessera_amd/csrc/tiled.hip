@@ -1,0 +1,257 @@
+// "tiled": out[m, n] = after(sum_k x[m, k] w[n, k]) for many rows.
+//
+// Replaces the reference's matrix-unit matmul rule (engine/rules/linear/src/
+// tiled.rs:281-345 tiled, :186-278 tiled_parts, :441-453, :611-672 propose),
+// which on gfx950 is refused today (no tile row for gfx9_5). Same product and
+// fused stages (engine/plan/lower/src/kernels/map.rs:155-185).
+//
+// gfx950 design:
+//  * 128x128 output tile per 256-thread group (4 waves in 2x2, each 64x64 =
+//    4x4 v_mfma_f32_16x16x32_bf16 tiles), k in 64-deep steps.
+//  * Both operands are k-contiguous ([m,k] and [n,k]), which is the matrix
+//    unit's native operand order: a lane's 8 k values are one 16-byte LDS read.
+//  * LDS holds two stages (A and B, 16 KiB each per stage, plus a second A
+//    stage for the low part of f32 rows); the next k-step is fetched from HBM
+//    into registers while the current one multiplies, then stored to the other
+//    stage: one barrier per k-step.
+//  * LDS rows are 128 bytes (8 chunks of 16B); chunk c of row r sits at chunk
+//    c ^ (r & 7), so the 16 rows one MFMA operand read touches spread over all
+//    banks instead of hitting one.
+//  * f32 rows are split into two exact bf16 parts (as tiled_parts does with
+//    three), e4m3 weights decode to bf16 on the way into LDS with the per-row
+//    scale applied to the finished sum; SiLU-gate pairs are laid out so a lane
+//    holds gate and up of the same column.
+#include "common.h"
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int kThreads = 256;
+
+struct TiledParams {
+    const void *x;
+    const void *w;
+    const uint16_t *w_scale;
+    const float *a0;
+    void *out;
+    uint32_t m, n, k;
+    uint32_t stages;
+    int out_bf16;
+};
+
+// Byte offset of (row, chunk) in a swizzled [128 rows][8 chunks of 16B] tile.
+TS_DEV uint32_t swz(uint32_t row, uint32_t chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
+
+template <bool XF32, bool W8, bool SILU>
+struct Loader {
+    // Per thread per stage: A: 4 chunks (rows t/8 + 32i, chunk t%8), B: 4 chunks.
+    u32x4 a_hi[4], a_lo[4], b[4];
+
+    // Weight row of B-tile row `br` for this output tile.
+    TS_DEV static uint32_t wrow(uint32_t br, uint32_t n0, uint32_t N) {
+        if (!SILU) return n0 + br;
+        const uint32_t half = br >> 6, within = br & 63;
+        return within < 32 ? n0 + half * 32 + within : N + n0 + half * 32 + (within - 32);
+    }
+
+    TS_DEV void fetch(const TiledParams &p, uint32_t m0, uint32_t n0, uint32_t k0) {
+        const uint32_t t = threadIdx.x, chunk = t & 7;
+        const uint32_t kk = k0 + chunk * 8;
+        const bool kin = kk < p.k;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = (t >> 3) + 32 * i;
+            const uint32_t m = m0 + r;
+            if (XF32) {
+                float v[8];
+                if (m < p.m && kin) {
+                    const float4 *src = (const float4 *)((const float *)p.x + (size_t)m * p.k + kk);
+                    float4 u0 = src[0], u1 = src[1];
+                    v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+                    v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) v[e] = 0.0f;
+                }
+                uint32_t h[4], l[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float x0 = v[2 * e], x1 = v[2 * e + 1];
+                    float h0 = bf16_round(x0), h1 = bf16_round(x1);
+                    h[e] = pack_bf16x2(h0, h1);
+                    l[e] = pack_bf16x2(x0 - h0, x1 - h1);
+                }
+                a_hi[i] = u32x4{h[0], h[1], h[2], h[3]};
+                a_lo[i] = u32x4{l[0], l[1], l[2], l[3]};
+            } else {
+                a_hi[i] = (m < p.m && kin) ? *(const u32x4 *)((const uint16_t *)p.x + (size_t)m * p.k + kk)
+                                           : u32x4{0, 0, 0, 0};
+            }
+            const uint32_t nr = wrow(r, n0, p.n);
+            const uint32_t nrows = SILU ? 2 * p.n : p.n;
+            const bool nin = (SILU ? (n0 + (r >> 6) * 32 + (r & 31)) < p.n : nr < nrows) && kin;
+            if (W8) {
+                if (nin) {
+                    const u32x2 c = *(const u32x2 *)((const uint8_t *)p.w + (size_t)nr * p.k + kk);
+                    u32x2 lo = e4m3x4_to_bf16x4(c.x), hi = e4m3x4_to_bf16x4(c.y);
+                    b[i] = u32x4{lo.x, lo.y, hi.x, hi.y};
+                } else {
+                    b[i] = u32x4{0, 0, 0, 0};
+                }
+            } else {
+                b[i] = nin ? *(const u32x4 *)((const uint16_t *)p.w + (size_t)nr * p.k + kk) : u32x4{0, 0, 0, 0};
+            }
+        }
+    }
+
+    TS_DEV void store(char *sa, char *sa_lo, char *sb) {
+        const uint32_t t = threadIdx.x, chunk = t & 7;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = (t >> 3) + 32 * i;
+            *(u32x4 *)(sa + swz(r, chunk)) = a_hi[i];
+            if (XF32) *(u32x4 *)(sa_lo + swz(r, chunk)) = a_lo[i];
+            *(u32x4 *)(sb + swz(r, chunk)) = b[i];
+        }
+    }
+};
+
+template <bool XF32, bool W8, bool SILU>
+__global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
+    constexpr int TILE = BM * BK * 2;  // bytes of one operand stage
+    __shared__ __attribute__((aligned(16))) char lds[2][XF32 ? 3 : 2][TILE];
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t col = lane & 15, grp = lane >> 4;
+    const uint32_t m0 = blockIdx.y * BM;
+    const uint32_t n0 = blockIdx.x * (SILU ? BN / 2 : BN);  // SILU: 64 output columns per tile
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    Loader<XF32, W8, SILU> ld;
+    const uint32_t steps = (p.k + BK - 1) / BK;
+    ld.fetch(p, m0, n0, 0);
+    ld.store(lds[0][0], lds[0][XF32 ? 2 : 0], lds[0][1]);
+    __syncthreads();
+
+    for (uint32_t s = 0; s < steps; s++) {
+        const int cur = s & 1;
+        if (s + 1 < steps) ld.fetch(p, m0, n0, (s + 1) * BK);
+        const char *sa = lds[cur][0], *sb = lds[cur][1], *sl = lds[cur][XF32 ? 2 : 0];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const uint32_t chunk = ks * 4 + grp;
+            bf16x8 af[4], al[4], bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t ra = wm * 64 + i * 16 + col;
+                af[i] = as_bf16x8(*(const u32x4 *)(sa + swz(ra, chunk)));
+                if (XF32) al[i] = as_bf16x8(*(const u32x4 *)(sl + swz(ra, chunk)));
+                const uint32_t rb = wn * 64 + i * 16 + col;
+                bfr[i] = as_bf16x8(*(const u32x4 *)(sb + swz(rb, chunk)));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+                    if (XF32) acc[i][j] = mfma16(al[i], bfr[j], acc[i][j]);
+                }
+        }
+        if (s + 1 < steps) {
+            const int nxt = cur ^ 1;
+            ld.store(lds[nxt][0], lds[nxt][XF32 ? 2 : 0], lds[nxt][1]);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue. D lane layout: column col, rows 4*grp + r of each 16x16 tile.
+    const uint32_t N = p.n, M = p.m;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t m = m0 + wm * 64 + i * 16 + 4 * grp + r;
+            if (m >= M) continue;
+            if (!SILU) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t n = n0 + wn * 64 + j * 16 + col;
+                    if (n >= N) continue;
+                    float v = acc[i][j][r];
+                    if (W8) v *= bf16_float(p.w_scale[n]);
+                    if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
+                    if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
+                    else ((float *)p.out)[(size_t)m * N + n] = v;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t n = n0 + wn * 32 + j * 16 + col;
+                    if (n >= N) continue;
+                    float g = acc[i][j][r], u = acc[i][j + 2][r];
+                    if (W8) {
+                        g *= bf16_float(p.w_scale[n]);
+                        u *= bf16_float(p.w_scale[N + n]);
+                    }
+                    float v = g / (1.0f + expf(-g)) * u;
+                    if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
+                    if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
+                    else ((float *)p.out)[(size_t)m * N + n] = v;
+                }
+            }
+        }
+    }
+}
+
+using Kern = void (*)(TiledParams);
+
+template <bool XF32, bool W8>
+Kern pick(bool silu) {
+    return silu ? tiled_kernel<XF32, W8, true> : tiled_kernel<XF32, W8, false>;
+}
+
+}  // namespace
+
+extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
+    TS_REQUIRE(a && a->x && a->w && a->out, "tiled: null pointer");
+    TS_REQUIRE(a->m >= 1 && a->n >= 1 && a->k >= 1, "tiled: empty product m=%u n=%u k=%u", a->m, a->n, a->k);
+    TS_REQUIRE(a->k % 8 == 0, "tiled: k=%u must be a multiple of 8", a->k);
+    TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "tiled: x dtype %d", a->x_dtype);
+    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3, "tiled: w dtype %d", a->w_dtype);
+    TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "tiled: out dtype %d", a->out_dtype);
+    TS_REQUIRE(a->w_dtype != TS_E4M3 || a->w_scale, "tiled: e4m3 weights need w_scale");
+    TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "tiled: TS_AFTER_ADD needs a0");
+    TS_REQUIRE(!(a->stages & TS_BEFORE_RMS_NORM), "tiled: RmsNorm prologue is fused only for m <= 16");
+    TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL)) == 0, "tiled: unknown stage bits %#x",
+               a->stages);
+    TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "tiled: x and w must be 16-byte aligned");
+    const bool silu = a->stages & TS_AFTER_SILU_MUL;
+    TiledParams p;
+    p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;
+    p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
+    const uint32_t cols = silu ? BN / 2 : BN;
+    const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->m + BM - 1) / BM;
+    TS_REQUIRE(gy <= 65535, "tiled: m=%u too large for one launch", a->m);
+    const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
+    Kern k = xf ? (w8 ? pick<true, true>(silu) : pick<true, false>(silu))
+                : (w8 ? pick<false, true>(silu) : pick<false, false>(silu));
+    hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
+    TS_CHECK_LAUNCH("tiled launch");
+    return TS_OK;
+}
+
+extern "C" size_t tessera_hip_linear_workspace(const ts_linear_args *a) {
+    if (!a) return 0;
+    return a->m <= 16 ? tessera_hip_lanes_workspace(a) : 0;
+}
+
+extern "C" int tessera_hip_linear(const ts_linear_args *a, void *stream) {
+    TS_REQUIRE(a, "linear: null args");
+    return a->m <= 16 ? tessera_hip_lanes(a, stream) : tessera_hip_tiled(a, stream);
+}

@@ -1,0 +1,189 @@
+"""Host-side mirror of the reference's lowering-rule kernels, over torch device tensors.
+
+Each function is named for the reference rule whose kernel it launches
+(``tiled``, ``lanes``, ``linear``, ``attend_rows``, ``flash_rows``, ``rms_norm``,
+``rope``, ``argmax``, ``top_k``, ``gather``) and takes the same operands in the
+same order as that rule's Launch (reads, epilogue operands, output, counts:
+engine/plan/lower/src/abi.rs:148-153, product.rs:70-76, rule.rs:92-110).
+torch only provides device memory and the current stream; every computation is
+a call into libtessera_hip.so through ``tessera_amd.abi``. Errors raise
+``abi.HipError`` with the library's message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import torch
+
+from . import abi
+
+_DT = {torch.float32: abi.TS_F32, torch.bfloat16: abi.TS_BF16, torch.uint8: abi.TS_E4M3,
+       torch.float8_e4m3fn: abi.TS_E4M3}
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+class Workspace:
+    """Caller-owned scratch for split-K / split-KV partials: grown on demand, zeroed
+    once when (re)allocated (the kernels return their counters to zero)."""
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes: int):
+        if nbytes == 0:
+            return None, 0
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+        return C.c_void_p(self.buf.data_ptr()), self.buf.numel()
+
+
+_ws = {}
+
+
+def workspace(device) -> Workspace:
+    key = str(device)
+    if key not in _ws:
+        _ws[key] = Workspace(device)
+    return _ws[key]
+
+
+def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6):
+    m, k = x.shape
+    n = out.shape[1]
+    a = abi.LinearArgs()
+    a.x, a.w, a.w_scale, a.gain, a.a0, a.out = (_ptr(x), _ptr(w), _ptr(w_scale), _ptr(gain), _ptr(a0),
+                                                _ptr(out))
+    a.m, a.n, a.k = m, n, k
+    a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
+    a.stages, a.eps = stages, eps
+    return a
+
+
+def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, gain=None, a0=None,
+            silu_mul=False, eps=1e-6):
+    m = x.shape[0]
+    n = w.shape[0] // 2 if silu_mul else w.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    stages = (abi.TS_AFTER_ADD if a0 is not None else 0) | (abi.TS_AFTER_SILU_MUL if silu_mul else 0) | \
+        (abi.TS_BEFORE_RMS_NORM if gain is not None else 0)
+    a = linear_args(x, w, out, w_scale=w_scale, gain=gain, a0=a0, stages=stages, eps=eps)
+    lib = abi.load()
+    need = getattr(lib, fn + "_workspace")(C.byref(a)) if hasattr(lib, fn + "_workspace") else 0
+    a.workspace, a.workspace_bytes = workspace(x.device).get(need)
+    abi.call(fn, C.byref(a), _stream())
+    return out
+
+
+def linear(x, w, **kw):
+    """tiled or lanes by row count (the cost select between the two rules)."""
+    return _linear("tessera_hip_linear", x, w, **kw)
+
+
+def lanes(x, w, **kw):
+    """Few-row product (rule "lanes"/"thin"): m <= 16."""
+    return _linear("tessera_hip_lanes", x, w, **kw)
+
+
+def tiled(x, w, **kw):
+    """Matrix-unit product (rule "tiled")."""
+    return _linear("tessera_hip_tiled", x, w, **kw)
+
+
+def rows_args(q, k, v, out, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
+              back=abi.U32_MAX, max_position=None):
+    rows, heads, width = q.shape
+    a = abi.RowsArgs()
+    a.q, a.k, a.v, a.out = _ptr(q), _ptr(k), _ptr(v), _ptr(out)
+    a.slots, a.positions, a.kept_table = _ptr(slots), _ptr(positions), _ptr(table)
+    a.rows, a.keys, a.heads, a.kv_heads, a.width = rows, keys, heads, k.shape[-2], width
+    a.back, a.kept_pages, a.page, a.scale = back, kept_pages, page, scale
+    a.q_dtype, a.kv_dtype, a.out_dtype = _DT[q.dtype], _DT[k.dtype], _DT[out.dtype]
+    if max_position is None:
+        max_position = int(positions.max().item()) if rows else 0
+    a.max_position = max_position
+    return a
+
+
+def attend_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
+                back=abi.U32_MAX, max_position=None, out=None):
+    """Decode rows over kept K/V (rule "attend"/attend_rows; split-KV)."""
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    a = rows_args(q, k, v, out, slots, positions, keys=keys, scale=scale, table=table,
+                  kept_pages=kept_pages, page=page, back=back, max_position=max_position)
+    need = abi.load().tessera_hip_attend_rows_workspace(C.byref(a))
+    a.workspace, a.workspace_bytes = workspace(q.device).get(need)
+    abi.call("tessera_hip_attend_rows", C.byref(a), _stream())
+    return out
+
+
+def flash_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
+               back=abi.U32_MAX, out=None):
+    """Prefill rows over kept K/V (rule "flash"/flash_rows)."""
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    a = rows_args(q, k, v, out, slots, positions, keys=keys, scale=scale, table=table,
+                  kept_pages=kept_pages, page=page, back=back, max_position=0)
+    abi.call("tessera_hip_flash_rows", C.byref(a), _stream())
+    return out
+
+
+def rms_norm(x, gain, eps, out=None):
+    rows, width = x.reshape(-1, x.shape[-1]).shape
+    if out is None:
+        out = torch.empty_like(x)
+    abi.call("tessera_hip_rms_norm", _ptr(x), _ptr(gain), _ptr(out), rows, width, C.c_float(eps), _stream())
+    return out
+
+
+def rope(x, positions, theta, halves=True):
+    """In place on x [rows, heads, width]."""
+    rows, heads, width = x.shape
+    abi.call("tessera_hip_rope", _ptr(x), _ptr(positions), rows, heads, width, C.c_float(theta),
+             1 if halves else 0, _stream())
+    return x
+
+
+def qk_norm_rope_append(qkv, q_gain, k_gain, q_out, k_cache, v_cache, slots, positions, *, heads,
+                        kv_heads, keys, eps, theta, table=None, kept_pages=0, page=16):
+    rows = qkv.shape[0]
+    abi.call("tessera_hip_qk_norm_rope_append", _ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(q_out),
+             _ptr(k_cache), _ptr(v_cache), _ptr(slots), _ptr(positions), _ptr(table), rows, heads, kv_heads,
+             128, keys, kept_pages, page, C.c_float(eps), C.c_float(theta), _stream())
+    return q_out
+
+
+def gather(table, ids, first=0, out=None):
+    count = ids.numel()
+    rows, width = table.shape
+    if out is None:
+        out = torch.empty((count, width), dtype=torch.float32, device=table.device)
+    abi.call("tessera_hip_gather", _ptr(table), _ptr(ids), _ptr(out), count, rows, width, first, _stream())
+    return out
+
+
+def argmax(x, ids=None):
+    rows, width = x.shape
+    if ids is None:
+        ids = torch.empty(rows, dtype=torch.int32, device=x.device)
+    need = abi.load().tessera_hip_argmax_workspace(rows, width)
+    ws, nbytes = workspace(x.device).get(need)
+    abi.call("tessera_hip_argmax", _ptr(x), _ptr(ids), rows, width, ws, nbytes, _stream())
+    return ids
+
+
+def top_k(x, k, ids=None):
+    rows, width = x.shape
+    if ids is None:
+        ids = torch.empty((rows, k), dtype=torch.int32, device=x.device)
+    abi.call("tessera_hip_top_k", _ptr(x), _ptr(ids), rows, width, k, _stream())
+    return ids

@@ -1,0 +1,52 @@
+"""CPU checks of the C ABI: the library loads, exports every declared function and
+rejects bad arguments before touching a device."""
+import ctypes as C
+
+from tessera_amd import abi
+
+
+def test_exports_every_declared_function():
+    lib = abi.load()
+    declared = abi.declared_functions()
+    assert len(declared) >= 18
+    for name in declared:
+        assert hasattr(lib, name), name
+        assert name in abi.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(abi.SIGNATURES) == set(declared)
+    arity = abi.declared_arity()
+    for name, (_, args) in abi.SIGNATURES.items():
+        assert arity[name] == len(args), (name, arity[name], len(args))
+    assert lib.tessera_hip_abi_version() == 1
+
+
+def test_argument_errors_need_no_device():
+    lib = abi.load()
+    a = abi.LinearArgs()
+    assert lib.tessera_hip_lanes(C.byref(a), None) == abi.TS_ERR_ARG
+    assert b"null" in lib.tessera_hip_last_error()
+    a.x = a.w = a.out = 16
+    a.m, a.n, a.k = 17, 8, 64
+    assert lib.tessera_hip_lanes(C.byref(a), None) == abi.TS_ERR_ARG
+    assert b"m=17" in lib.tessera_hip_last_error()
+    r = abi.RowsArgs()
+    r.q = r.k = r.v = r.out = r.slots = r.positions = 16
+    r.width, r.heads, r.kv_heads = 64, 16, 8
+    assert lib.tessera_hip_attend_rows(C.byref(r), None) == abi.TS_ERR_ARG
+    assert b"width 64" in lib.tessera_hip_last_error()
+    assert lib.tessera_hip_top_k(None, None, 1, 4, 2, None) == abi.TS_ERR_ARG
+
+
+def test_struct_layout_matches_header():
+    # Offsets the C compiler gives the header's structs (x86-64 SysV).
+    assert C.sizeof(abi.LinearArgs) == 8 * 8 + 4 * 8
+    assert abi.LinearArgs.m.offset == 64 and abi.LinearArgs.eps.offset == 92
+    assert abi.RowsArgs.rows.offset == 72 and abi.RowsArgs.max_position.offset == 120
+
+
+def test_workspace_sizes():
+    lib = abi.load()
+    a = abi.LinearArgs()
+    a.m, a.n, a.k = 1, 1024, 3072
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) > 0  # few tiles: split-K
+    a.n = 151936
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0

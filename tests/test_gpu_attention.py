@@ -1,0 +1,108 @@
+"""Parity of the attention kernels with the oracle's attend_rows over paged K/V.
+
+K/V are stored bf16 in the kept rows; the oracle reads the same bf16 values widened.
+Tolerance: |got - want| <= 2e-4 (outputs are convex combinations of N(0,1) V rows;
+q is carried in two exact bf16 parts, P in two parts for the prefill kernel, and
+the rest is f32 in another summation order).
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.helpers import bf16_bits_normal, from_dev, rng, to_dev
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+ATOL = 2e-4
+
+
+def paged_case(seed, ctxs, heads=16, kv_heads=8, page=16, pos=None):
+    """Kept rows for len(ctxs) slots in shuffled pages, one query row per slot at
+    ctx-1 (decode) unless `pos` gives each row's (slot, position)."""
+    r = rng(seed)
+    slots_n = len(ctxs)
+    kept_pages = max(math.ceil(c / page) for c in ctxs)
+    total = slots_n * kept_pages
+    table = r.permutation(total).astype(np.uint32)  # seeded shuffle of every page
+    kb, kf = bf16_bits_normal(r, (total * page, kv_heads, 128))
+    vb, vf = bf16_bits_normal(r, (total * page, kv_heads, 128))
+    if pos is None:
+        slots = np.arange(slots_n, dtype=np.uint32)
+        positions = np.array([c - 1 for c in ctxs], np.uint32)
+    else:
+        slots, positions = (np.array(a, np.uint32) for a in pos)
+    q = r.standard_normal((len(slots), heads, 128)).astype(np.float32)
+    return dict(q=q, kb=kb, kf=kf, vb=vb, vf=vf, table=table, slots=slots, positions=positions,
+                kept_pages=kept_pages, page=page, keys=kept_pages * page)
+
+
+def run(kernel, c, scale, back=0xFFFFFFFF):
+    from tessera_amd import rules as R
+    fn = R.attend_rows if kernel == "attend" else R.flash_rows
+    return from_dev(fn(to_dev(c["q"], torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                       to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                       keys=c["keys"], scale=scale, table=to_dev(c["table"], torch, torch.int32),
+                       kept_pages=c["kept_pages"], page=c["page"], back=back))
+
+
+def want(c, scale, mask="causal", n=0):
+    return O.attend_rows(c["q"], c["kf"], c["vf"], c["slots"], c["positions"], c["keys"], scale,
+                         mask=mask, n=n, table=c["table"], kept_pages=c["kept_pages"], page=c["page"])
+
+
+@pytest.mark.parametrize("ctxs", [[1], [17, 5, 33], [144], [512, 1000, 2049], [8192, 600]])
+def test_decode_rows_paged(ctxs):
+    c = paged_case(len(ctxs) * 100 + ctxs[0], ctxs)
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("attend", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
+def test_decode_rows_c3_sample():
+    """C3 decode shape on a subset of rows: contexts U[512, 8192] (seed 2)."""
+    ctxs = rng(2).integers(512, 8193, 8).tolist()
+    c = paged_case(2, ctxs)
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("attend", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (32, 8), (16, 1)])
+def test_decode_gqa_groups(heads, kv_heads):
+    c = paged_case(9 + heads, [300, 70], heads=heads, kv_heads=kv_heads)
+    np.testing.assert_allclose(run("attend", c, 0.1), want(c, 0.1), atol=ATOL, rtol=0)
+
+
+def test_decode_window():
+    c = paged_case(77, [400, 90])
+    got = run("attend", c, 0.2, back=31)
+    np.testing.assert_allclose(got, want(c, 0.2, "back", 31), atol=ATOL, rtol=0)
+
+
+def test_decode_many_rows_per_slot():
+    """Rows of one slot at several positions (a verify/prefill-like batch)."""
+    c = paged_case(5, [100], pos=([0, 0, 0, 0], [0, 15, 16, 99]))
+    np.testing.assert_allclose(run("attend", c, 0.3), want(c, 0.3), atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("lens", [[1], [64], [100], [130, 70], [2048]])
+def test_prefill_flash_rows(lens):
+    """Prefill: each slot's rows at positions 0..len-1, slots padded to 64-row blocks
+    apart (a 64-row block never crosses a slot)."""
+    slots, positions = [], []
+    for s, n in enumerate(lens):
+        slots += [s] * n
+        positions += list(range(n))
+        pad = (-n) % 64
+        if s + 1 < len(lens) and pad:
+            # fill with the same slot's last position again so blocks stay in one slot
+            slots += [s] * pad
+            positions += [n - 1] * pad
+    c = paged_case(sum(lens), lens, pos=(slots, positions))
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("flash", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
+def test_prefill_flash_window_and_gqa():
+    c = paged_case(8, [200], heads=8, kv_heads=2, pos=([0] * 200, list(range(200))))
+    np.testing.assert_allclose(run("flash", c, 0.25, back=40), want(c, 0.25, "back", 40), atol=ATOL, rtol=0)

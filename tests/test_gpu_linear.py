@@ -1,0 +1,139 @@
+"""Parity of the linear kernels (lanes, tiled) with the oracle's product.
+
+Tolerances (stated per test):
+  * f32 rows x bf16 weights, f32 out: |got - want| <= 1e-4 * (|x| @ |w|^T) + 1e-6
+    per element (x is carried as two exact bf16 parts, 16 mantissa bits, and the
+    matrix unit sums in a different order than the oracle's sequential f32 loop).
+  * bf16 rows (the C2 sweep): exact bf16 inputs, so the same bound applies to f32
+    out; bf16 out adds one bf16 rounding: max-rel <= 2e-2 (BASELINE tolerance).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from tests.helpers import bf16_bits_normal, from_dev, max_rel, rng, to_dev
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def _bound(x, w):
+    return 1e-4 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T) + 1e-6
+
+
+def _rules():
+    from tessera_amd import rules
+    return rules
+
+
+def _check(got, want, bound):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= bound), f"max err {err.max()} vs bound at argmax {bound.reshape(-1)[err.argmax()]}"
+
+
+# tiles_match_cpu sizes (engine/rules/linear/tests/tiled_test.rs:58-71) plus decode rows.
+SHAPES = [(1, 3, 4), (37, 50, 72), (64, 64, 64), (600, 40, 512), (256, 512, 1024),
+          (1, 2048, 1024), (4, 1024, 3072), (16, 6144, 1024), (3, 100, 200)]
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES)
+def test_linear_f32_rows_bf16_weights(m, n, k):
+    R = _rules()
+    r = rng(29 + m + n + k)
+    x = r.standard_normal((m, k)).astype(np.float32)
+    wb, wf = bf16_bits_normal(r, (n, k), 0.02)
+    want = O.product_bf16w(x, wb)
+    got = from_dev(R.linear(to_dev(x, torch), to_dev(wb, torch)))
+    _check(got, want, _bound(x, wf))
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 128])
+@pytest.mark.parametrize("k,n", [(1024, 2048), (2048, 1024), (3072, 1024)])
+def test_linear_bf16_sweep_shapes(m, k, n):
+    """C2: N(0,1) bf16 x and w, f32 accumulate, bf16 and f32 out."""
+    R = _rules()
+    r = rng(m * 7 + k + n)
+    xb, xf = bf16_bits_normal(r, (m, k))
+    wb, wf = bf16_bits_normal(r, (n, k))
+    want = O.product_bf16w(xf, wb)
+    got = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch)))
+    _check(got, want, _bound(xf, wf))
+    got16 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), out_dtype=torch.bfloat16))
+    assert max_rel(got16, want) <= 2e-2
+
+
+def test_lanes_and_tiled_agree_at_16_rows():
+    R = _rules()
+    r = rng(5)
+    x = r.standard_normal((16, 512)).astype(np.float32)
+    wb, wf = bf16_bits_normal(r, (300, 512), 0.05)
+    a = from_dev(R.lanes(to_dev(x, torch), to_dev(wb, torch)))
+    b = from_dev(R.tiled(to_dev(x, torch), to_dev(wb, torch)))
+    _check(a, b, _bound(x, wf))
+
+
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_fused_stages(m):
+    """RmsNorm before (lanes only), SiLU*up and the residual add after."""
+    R = _rules()
+    r = rng(11 + m)
+    k, n = 256, 96
+    x = r.standard_normal((m, k)).astype(np.float32)
+    g = (1.0 + 0.02 * r.standard_normal(k)).astype(np.float32)
+    wb, wf = bf16_bits_normal(r, (2 * n, k), 0.05)
+    res = r.standard_normal((m, n)).astype(np.float32)
+    # silu(gate) * up, then + residual (engine/models/src/shared.rs:375-378; map.rs:93-96)
+    gu = O.product_bf16w(x, wb)
+    want = O.act("silu", gu[:, :n]) * gu[:, n:] + res
+    got = from_dev(R.linear(to_dev(x, torch), to_dev(wb, torch), silu_mul=True, a0=to_dev(res, torch)))
+    # First-order error of silu(g)*u: |silu'| <= 1.1, |silu(g)| <= |g|.
+    b = _bound(x, wf)
+    _check(got, want, 1.1 * b[:, :n] * np.abs(gu[:, n:]) + np.abs(gu[:, :n]) * b[:, n:] + 1e-5)
+    if m <= 16:
+        xn = O.rms_norm(x, g, 1e-6)
+        want2 = O.product_bf16w(xn, wb[:n])
+        got2 = from_dev(R.linear(to_dev(x, torch), to_dev(wb[:n], torch), gain=to_dev(g, torch), eps=1e-6))
+        _check(got2, want2, 2 * _bound(xn, wf[:n]))
+
+
+def test_residual_in_place():
+    R = _rules()
+    r = rng(3)
+    x = r.standard_normal((1, 1024)).astype(np.float32)
+    wb, wf = bf16_bits_normal(r, (1024, 1024), 0.02)
+    h = r.standard_normal((1, 1024)).astype(np.float32)
+    hd = to_dev(h, torch)
+    R.linear(to_dev(x, torch), to_dev(wb, torch), a0=hd, out=hd)
+    _check(from_dev(hd), O.product_bf16w(x, wb) + h, _bound(x, wf) + 1e-6)
+
+
+def _quantize(r, n, k):
+    """C4 weights: N(0,0.02) rows, scale = absmax/448 as bf16, codes = e4m3(w/s)."""
+    w = (r.standard_normal((n, k)) * 0.02).astype(np.float32)
+    s_bits = O.bf16_narrow((np.abs(w).max(1) / 448.0).astype(np.float32))
+    s = O.bf16_widen(s_bits)
+    codes = O.e4m3_narrow(w / s[:, None])
+    return codes, s_bits
+
+
+@pytest.mark.parametrize("m", [1, 8, 64])
+def test_e4m3_weights(m):
+    R = _rules()
+    r = rng(40 + m)
+    k, n = 1024, 512
+    codes, s_bits = _quantize(r, n, k)
+    xb, xf = bf16_bits_normal(r, (m, k))
+    want = O.product_e4m3w(xf, codes, s_bits)
+    wdeq = O.e4m3_widen(codes) * O.bf16_widen(s_bits)[:, None]
+    got = from_dev(R.linear(to_dev(xb, torch), to_dev(codes, torch), w_scale=to_dev(s_bits, torch)))
+    _check(got, want, _bound(xf, wdeq))
+
+
+def test_argument_errors_raise():
+    R = _rules()
+    from tessera_amd import abi
+    x = torch.zeros((17, 64), device="cuda")
+    w = torch.zeros((8, 64), device="cuda", dtype=torch.bfloat16)
+    with pytest.raises(abi.HipError) as e:
+        R.lanes(x, w)
+    assert e.value.code == abi.TS_ERR_ARG and "m=17" in str(e.value)
