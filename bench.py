@@ -1,0 +1,183 @@
+"""Headline benchmark: Qwen3-0.6B-shaped bf16 decode at batch 1 on one MI355X.
+
+A "step" is one greedy decode token (all 28 layers, the tied lm_head and argmax)
+replayed from the runner's HIP graph, with weights, kept rows and the token already
+resident in HBM. The timed run is the C1 workload: a 128-token prompt (seed 1), then
+K decode steps (K=32: context 128..160). Warmup runs W steps of an earlier
+generation first. Prints one JSON line.
+
+Also measured in the same run:
+  * roofline of the dominant kernel (lanes on the lm_head shape: 151936 x 1024 bf16,
+    311 MB per launch) timed with HIP events on the stream it runs on;
+  * the whole step against HBM: 1,192,099,840 weight bytes + 114,688 B per kept
+    position per token;
+  * prefill GEMMs (M=2048, the C2 projection shapes) as a fraction of bf16 MFMA peak;
+  * the CPU baseline: the oracle (a C restatement of tessera-interp) decoding a bounded
+    sample of steps on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # B/s, MI355X
+BF16_PEAK = 2.5e15         # FLOP/s dense, MI355X
+WEIGHT_BYTES = 596_049_920 * 2
+KV_BYTES_PER_POS = 28 * 2 * 8 * 128 * 2
+PROMPT = 128
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=32)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--cpu-steps", type=int, default=8)
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-gemm", action="store_true")
+    return p.parse_args()
+
+
+def lm_head_roofline(torch, reps=20):
+    """lanes on the lm_head shape, timed with HIP events on torch's current stream
+    (the stream rules.lanes launches on)."""
+    from tessera_amd import rules
+    n, k = 151936, 1024
+    g = torch.Generator(device="cuda").manual_seed(0)
+    w = (torch.randn((n, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn((1, k), device="cuda", generator=g)
+    gain = torch.ones(k, device="cuda")
+    out = torch.empty((1, n), device="cuda")
+    for _ in range(3):
+        rules.lanes(x, w, gain=gain, out=out)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        rules.lanes(x, w, gain=gain, out=out)
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / reps
+    nbytes = n * k * 2 + k * 4 * 2 + n * 4  # weights, x and gain, logits
+    return {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": nbytes / t / HBM_PEAK, "traffic": None, "kernel": "lanes_kernel (lm_head 151936x1024)",
+            "bytes_per_launch": nbytes, "us_per_launch": t * 1e6}
+
+
+def gemm_sweep(torch, reps=10):
+    """C2 at M=2048: bf16 x and w, f32 accumulate, bf16 out; TFLOP/s per shape."""
+    from tessera_amd import rules
+    shapes = {"q": (1024, 2048), "kv": (1024, 1024), "o": (2048, 1024), "gate_up": (1024, 6144),
+              "down": (3072, 1024), "lm_head": (1024, 151936)}
+    M = 2048
+    res, flops_all, t_all = {}, 0.0, 0.0
+    for name, (K, N) in shapes.items():
+        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+        w = torch.randn((N, K), device="cuda").to(torch.bfloat16)
+        out = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        for _ in range(2):
+            rules.tiled(x, w, out=out)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            rules.tiled(x, w, out=out)
+        e.record()
+        torch.cuda.synchronize()
+        t = s.elapsed_time(e) / 1e3 / reps
+        fl = 2.0 * M * N * K
+        res[name] = {"us": round(t * 1e6, 2), "tflops": round(fl / t / 1e12, 1), "frac": round(fl / t / BF16_PEAK, 4)}
+        flops_all += fl
+        t_all += t
+        del x, w, out
+    return {"M": M, "shapes": res, "aggregate_frac": round(flops_all / t_all / BF16_PEAK, 4)}
+
+
+def cpu_baseline(model, prompt, steps):
+    """The oracle decoding `steps` tokens after the same prompt, kept rows copied from
+    the device after its prefill; all host cores (up to 16) via OpenMP."""
+    import numpy as np
+
+    import oracle as O
+    from oracle.qwen3 import Qwen3 as OracleQwen3, from_runner
+    threads = min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    ref = OracleQwen3(from_runner(model))
+    c = model.config
+    for l in range(c.layers):
+        k = O.bf16_widen(model.read("k_cache", l)).reshape(-1, c.kv_heads, c.head_dim)
+        v = O.bf16_widen(model.read("v_cache", l)).reshape(-1, c.kv_heads, c.head_dim)
+        pages = model.pages((PROMPT + c.page - 1) // c.page)
+        for i in range(PROMPT):
+            row = pages[i // c.page] * c.page + i % c.page
+            ref.kv[l]["k"][i] = k[row]
+            ref.kv[l]["v"][i] = v[row]
+    tok = int(np.argmax(model.logits()))
+    t0 = time.perf_counter()
+    for i in range(steps):
+        logits = ref.forward([tok], [PROMPT + i])
+        tok = int(np.argmax(logits))
+    dt = time.perf_counter() - t0
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} greedy decode steps at context {PROMPT}..{PROMPT + steps} "
+                      f"(oracle restatement of tessera-interp, OpenMP over output columns, {threads} threads)"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path (asked for --gpus {a.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from tessera_amd.qwen3 import Qwen3, default_config
+    cfg = default_config(max_context=PROMPT + max(a.steps, a.warmup) + 1, max_prompt=PROMPT)
+    m = Qwen3(cfg, seed=0)
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, PROMPT).astype(np.uint32)
+    if a.warmup:
+        m.prefill(prompt)
+        m.decode(a.warmup)
+    torch.cuda.synchronize()
+    m.prefill(prompt)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    toks = m.decode(a.steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = a.steps / dt
+    mean_ctx = PROMPT + (a.steps + 1) / 2
+    step_bytes = WEIGHT_BYTES + KV_BYTES_PER_POS * mean_ctx
+    roof = lm_head_roofline(torch)
+    extra = {"step_hbm_frac": round(step_bytes * tok_s / HBM_PEAK, 4),
+             "step_bytes": int(step_bytes),
+             "roofline_tok_s": round(HBM_PEAK / step_bytes, 1),
+             "tokens_head": [int(t) for t in toks[:8]]}
+    if not a.no_gemm:
+        extra["prefill_gemm"] = gemm_sweep(torch)
+    cpu = None
+    if not a.no_cpu and a.cpu_steps > 0:
+        cpu = cpu_baseline(m, prompt, a.cpu_steps)
+    line = {
+        "metric": "decode tok/s + % HBM roofline (Qwen3-0.6B-shape b=1); prefill GEMM % MFMA peak",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+        "ms_per_step": round(dt / a.steps * 1e3, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,0.02) bf16 weights, uniform random 128-token prompt (seed 1)",
+        "config": {"workload": "C1 Qwen3-0.6B-shaped decode, batch 1, 128-token prompt then greedy steps",
+                   "global_batch": 1, "seq_len": PROMPT + a.steps, "parallelism": "none (1 GPU)"},
+        "roofline": roof, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    m.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -97,10 +97,11 @@ EXPORT uint16_t or_bf16_narrow(float x) { return (uint16_t)narrow_fmt(x, 8, 7, 1
 /* bf16 widening is exact: the top half of an f32. The general form above is the pinned
  * one; the shift is what the hot loops use, and the tests check both agree on all codes. */
 EXPORT float or_bf16_widen_exact(uint16_t b) { return widen_fmt(b, 8, 7, 1, 1); }
-EXPORT float or_bf16_widen(uint16_t b) {
+static inline float widen16(uint16_t b) {
     float f = u2f((uint32_t)b << 16);
     return isnan(f) ? NAN : f;
 }
+EXPORT float or_bf16_widen(uint16_t b) { return widen16(b); }
 EXPORT uint8_t or_e4m3_narrow(float x) { return (uint8_t)narrow_fmt(x, 4, 3, 0, 1); }
 EXPORT float or_e4m3_widen(uint8_t b) { return widen_fmt(b, 4, 3, 0, 1); }
 
@@ -159,16 +160,55 @@ EXPORT void or_product(int64_t m, int64_t n, int64_t k, const float *x, const fl
         for (int64_t r = 0; r < m; r++) out[r * n + c] = dot_f32(x + r * k, w + c * k, k);
 }
 
-/* The same product with w stored bf16 and widened per element (run.rs:232-237). */
+/* The same product with w stored bf16 and widened per element (run.rs:232-237).
+ * Eight rows share each widened weight row; each output keeps its own
+ * accumulator and ascending-k order, so the result equals one dot per output. */
+static void rows_dot(int64_t m, int64_t n, int64_t k, const float *x, const float *row, float *out, int64_t c) {
+    int64_t r = 0;
+    for (; r + 8 <= m; r += 8) {
+        float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int64_t i = 0; i < k; i++) {
+            const float w = row[i];
+            for (int j = 0; j < 8; j++) s[j] = s[j] + x[(r + j) * k + i] * w;
+        }
+        for (int j = 0; j < 8; j++) out[(r + j) * n + c] = s[j];
+    }
+    for (; r < m; r++) out[r * n + c] = dot_f32(x + r * k, row, k);
+}
+
+/* Few rows: eight columns at a time, each with its own accumulator. */
+static void cols_dot(int64_t m, int64_t n, int64_t k, const float *x, const uint16_t *w, float *out, int64_t c0,
+                     float *rows) {
+    for (int j = 0; j < 8; j++)
+        for (int64_t i = 0; i < k; i++) rows[j * k + i] = widen16(w[(c0 + j) * k + i]);
+    for (int64_t r = 0; r < m; r++) {
+        float s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        const float *xr = x + r * k;
+        for (int64_t i = 0; i < k; i++)
+            for (int j = 0; j < 8; j++) s[j] = s[j] + xr[i] * rows[j * k + i];
+        for (int j = 0; j < 8; j++) out[r * n + c0 + j] = s[j];
+    }
+}
+
 EXPORT void or_product_bf16w(int64_t m, int64_t n, int64_t k, const float *x, const uint16_t *w,
                              float *out) {
     #pragma omp parallel num_threads(g_threads) if (g_threads > 1)
     {
-        float *row = (float *)malloc(sizeof(float) * (size_t)k);
-        #pragma omp for schedule(static)
-        for (int64_t c = 0; c < n; c++) {
-            for (int64_t i = 0; i < k; i++) row[i] = or_bf16_widen(w[c * k + i]);
-            for (int64_t r = 0; r < m; r++) out[r * n + c] = dot_f32(x + r * k, row, k);
+        float *row = (float *)malloc(sizeof(float) * (size_t)k * 8);
+        if (m < 8) {
+            #pragma omp for schedule(static)
+            for (int64_t b = 0; b < n / 8; b++) cols_dot(m, n, k, x, w, out, b * 8, row);
+            #pragma omp single
+            for (int64_t c = n / 8 * 8; c < n; c++) {
+                for (int64_t i = 0; i < k; i++) row[i] = widen16(w[c * k + i]);
+                rows_dot(m, n, k, x, row, out, c);
+            }
+        } else {
+            #pragma omp for schedule(static)
+            for (int64_t c = 0; c < n; c++) {
+                for (int64_t i = 0; i < k; i++) row[i] = widen16(w[c * k + i]);
+                rows_dot(m, n, k, x, row, out, c);
+            }
         }
         free(row);
     }

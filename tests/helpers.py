@@ -37,3 +37,17 @@ def cosine(a, b):
     a = a.astype(np.float64).reshape(-1)
     b = b.astype(np.float64).reshape(-1)
     return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def host_weights(model):
+    from oracle.qwen3 import from_runner
+    return from_runner(model)
+
+
+def greedy_agrees(token, want_logits, tol):
+    """The device's greedy token matches the oracle's, or the oracle's top two are
+    within `tol` of each other (a near-tie that summation order may flip)."""
+    best = int(np.argmax(want_logits))
+    if token == best:
+        return True
+    return float(want_logits[best] - want_logits[token]) <= tol
