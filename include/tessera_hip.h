@@ -9,9 +9,8 @@
  *    for the null stream), so every call may be captured into a HIP graph.
  *  - Scratch (split-K / split-KV partials) comes from a caller-owned
  *    `workspace` of at least the bytes the matching *_workspace() call reports.
- *    Its first 256 KiB hold completion counters that must be zero before first
- *    use; every kernel returns the counters it used to zero, so one workspace,
- *    zeroed once, serves any sequence of stream-ordered calls. Calls that run
+ *    It carries nothing between calls (no counters, no state), so one
+ *    workspace serves any sequence of stream-ordered calls; calls that run
  *    concurrently (different streams) need separate workspaces.
  *  - Return 0 on success; a positive value is a passed-through hipError_t; a
  *    negative value is an argument error (TS_ERR_*). The message for the last

@@ -18,14 +18,17 @@
 //  * Online softmax per head in registers (16-lane butterflies), then P*V on
 //    the vector ALUs: a lane owns 2 adjacent head dims, so each V row is one
 //    256-byte coalesced load across the wave.
-//  * Partitions are merged (max, sum, acc) in LDS across the group's 4 waves and
-//    in the workspace across groups, the last group to finish combining them in
-//    partition order.
+//  * A group's waves (up to 16) split its keys and merge (max, sum, acc) in LDS.
+//    Short contexts (the batch-1 decode) take one group per (row, kv head).
+//    Long ones split keys across groups too: each writes its partial to the
+//    workspace and a second small kernel merges them in partition order. A
+//    kernel boundary orders the two: a device-wide fence inside one kernel costs
+//    more than the merge launch.
 #include "common.h"
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kMaxWaves = 16;
 constexpr int kMaxG = 16;
 
 struct RowsParams {
@@ -33,8 +36,7 @@ struct RowsParams {
     const uint16_t *k, *v;
     float *out;
     const uint32_t *slots, *positions, *table;
-    float *partials;     // [rows][kv_heads][parts][G][2 + 128]
-    uint32_t *counters;  // [rows][kv_heads]
+    float *partials;     // [rows][kv_heads][parts][G][2 + 128] when split across groups
     uint32_t rows, keys, heads, kv_heads, G, back, kept_pages, page_shift;
     uint32_t wave_keys;  // keys per wave per partition (multiple of 16)
     float scale;
@@ -47,8 +49,9 @@ TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
 }
 
 template <int G>
-__global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams p) {
+    constexpr int kWaves = (64 / G) < kMaxWaves ? (64 / G) : kMaxWaves;  // LDS bound: waves x G <= 64
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     const uint32_t part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z, parts = gridDim.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
 
@@ -56,7 +59,6 @@ __global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) 
     __shared__ float salpha[kWaves][G];
     __shared__ float sm[kWaves][G], sl[kWaves][G];
     __shared__ float so[kWaves][G][128];
-    __shared__ uint32_t last_s;
 
     const uint32_t pos = p.positions[r], slot = p.slots[r];
     const uint32_t from = pos > p.back ? pos - p.back : 0;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) 
 #pragma unroll
     for (int h = 0; h < G; h++) { o0[h] = 0.0f; o1[h] = 0.0f; }
 
-    const uint32_t wk0 = (part * kWaves + wave) * p.wave_keys;
+    const uint32_t wk0 = (part * waves + wave) * p.wave_keys;
     const uint32_t blocks = p.wave_keys / 16;
     for (uint32_t b = 0; b < blocks; b++) {
         const uint32_t kb = wk0 + 16 * b;
@@ -178,9 +180,9 @@ __global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) 
     for (uint32_t e = t; e < G * 128; e += blockDim.x) {
         const uint32_t h = e / 128, d = e % 128;
         float M = -INFINITY;
-        for (int w = 0; w < kWaves; w++) M = fmaxf(M, sm[w][h]);
+        for (uint32_t w = 0; w < waves; w++) M = fmaxf(M, sm[w][h]);
         float L = 0.0f, O = 0.0f;
-        for (int w = 0; w < kWaves; w++) {
+        for (uint32_t w = 0; w < waves; w++) {
             const float f = (sm[w][h] == -INFINITY) ? 0.0f : expf(sm[w][h] - M);
             L += sl[w][h] * f;
             O += so[w][h][d] * f;
@@ -192,43 +194,44 @@ __global__ __launch_bounds__(kWaves * 64) void attend_rows_kernel(RowsParams p) 
             if (d == 0) { mine[h * 130] = M; mine[h * 130 + 1] = L; }
         }
     }
-    if (parts == 1) return;
-    __threadfence();
-    __syncthreads();
-    if (t == 0) last_s = atomicAdd(&p.counters[gi], 1u) == parts - 1;
-    __syncthreads();
-    if (!last_s) return;
-    __threadfence();
+}
+
+// Merges the partitions of one (row, kv head) in partition order.
+template <int G>
+__global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t parts) {
+    const uint32_t kvh = blockIdx.x, r = blockIdx.y;
+    const size_t gi = (size_t)r * p.kv_heads + kvh;
     const float *all = p.partials + gi * parts * G * 130;
-    for (uint32_t e = t; e < G * 128; e += blockDim.x) {
+    for (uint32_t e = threadIdx.x; e < G * 128; e += blockDim.x) {
         const uint32_t h = e / 128, d = e % 128;
         float M = -INFINITY;
-        for (uint32_t q = 0; q < parts; q++) M = fmaxf(M, __builtin_nontemporal_load(all + (q * G + h) * 130));
+        for (uint32_t q = 0; q < parts; q++) M = fmaxf(M, all[(q * G + h) * 130]);
         float L = 0.0f, O = 0.0f;
         for (uint32_t q = 0; q < parts; q++) {
             const float *pq = all + (q * G + h) * 130;
-            const float mq = __builtin_nontemporal_load(pq);
-            const float f = (mq == -INFINITY) ? 0.0f : expf(mq - M);
-            L += __builtin_nontemporal_load(pq + 1) * f;
-            O += __builtin_nontemporal_load(pq + 2 + d) * f;
+            const float f = (pq[0] == -INFINITY) ? 0.0f : expf(pq[0] - M);
+            L += pq[1] * f;
+            O += pq[2 + d] * f;
         }
         p.out[((size_t)r * p.heads + kvh * G + h) * 128 + d] = O / L;
     }
-    if (t == 0) p.counters[gi] = 0;
 }
 
 struct Split {
-    uint32_t wave_keys, parts;
+    uint32_t wave_keys, parts, waves;
 };
 
 Split split(const ts_rows_args *a) {
+    const uint32_t G = a->heads / a->kv_heads;
+    const uint32_t waves = (64 / G) < (uint32_t)kMaxWaves ? 64 / G : kMaxWaves;
     const uint32_t span = a->max_position + 1;
-    uint32_t wave_keys = 64;
-    if (span <= 1024) wave_keys = 16;
-    else if (span <= 4096) wave_keys = 32;
     Split s;
-    s.wave_keys = wave_keys;
-    s.parts = (span + kWaves * wave_keys - 1) / (kWaves * wave_keys);
+    s.waves = waves;
+    // Keys per wave (a multiple of 16): as few as cover the span with one group.
+    s.wave_keys = 16;
+    while (s.wave_keys < 64 && s.wave_keys * waves < span) s.wave_keys *= 2;
+    s.parts = (span + waves * s.wave_keys - 1) / (waves * s.wave_keys);
+    if (s.parts == 1) s.waves = (span + s.wave_keys - 1) / s.wave_keys;
     return s;
 }
 
@@ -258,7 +261,7 @@ extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
     if (s.parts <= 1) return 0;
     const size_t G = a->heads / a->kv_heads;
     const size_t groups = (size_t)a->rows * a->kv_heads;
-    return kWsScratch + groups * s.parts * G * 130 * sizeof(float);
+    return groups * s.parts * G * 130 * sizeof(float);
 }
 
 extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
@@ -273,27 +276,28 @@ extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
     p.G = a->heads / a->kv_heads; p.back = a->back; p.kept_pages = a->kept_pages;
     p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
     p.wave_keys = s.wave_keys; p.scale = a->scale;
-    p.partials = nullptr; p.counters = nullptr;
+    p.partials = nullptr;
     if (s.parts > 1) {
         const size_t need = tessera_hip_attend_rows_workspace(a);
         if (!a->workspace || a->workspace_bytes < need)
             return ts::fail(TS_ERR_WORKSPACE, "attend_rows: workspace of %zu bytes needed", need);
-        const size_t groups = (size_t)a->rows * a->kv_heads;
-        TS_REQUIRE(groups <= kWsCounters, "attend_rows: %zu row x kv-head groups (at most %zu)", groups,
-                   kWsCounters);
-        p.counters = (uint32_t *)a->workspace;
-        p.partials = (float *)((char *)a->workspace + kWsScratch);
+        p.partials = (float *)a->workspace;
     }
     void (*k)(RowsParams) = nullptr;
+    void (*merge)(RowsParams, uint32_t) = nullptr;
     switch (p.G) {
-    case 1: k = attend_rows_kernel<1>; break;
-    case 2: k = attend_rows_kernel<2>; break;
-    case 4: k = attend_rows_kernel<4>; break;
-    case 8: k = attend_rows_kernel<8>; break;
-    case 16: k = attend_rows_kernel<16>; break;
+    case 1: k = attend_rows_kernel<1>; merge = attend_rows_merge<1>; break;
+    case 2: k = attend_rows_kernel<2>; merge = attend_rows_merge<2>; break;
+    case 4: k = attend_rows_kernel<4>; merge = attend_rows_merge<4>; break;
+    case 8: k = attend_rows_kernel<8>; merge = attend_rows_merge<8>; break;
+    case 16: k = attend_rows_kernel<16>; merge = attend_rows_merge<16>; break;
     default: return ts::fail(TS_ERR_ARG, "attend_rows: %u query heads per kv head (1, 2, 4, 8 or 16)", p.G);
     }
-    hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(s.waves * 64), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("attend_rows launch");
+    if (s.parts > 1) {
+        hipLaunchKernelGGL(merge, dim3(a->kv_heads, a->rows), dim3(256), 0, (hipStream_t)stream, p, s.parts);
+        TS_CHECK_LAUNCH("attend_rows merge launch");
+    }
     return TS_OK;
 }

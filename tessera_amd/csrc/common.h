@@ -15,11 +15,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define TS_DEV __device__ __forceinline__
 
-// Workspace layout shared by every entry point: counters first (zero at rest:
-// each kernel returns the ones it used to zero), scratch after. Keeping the
-// counters at a fixed place means one workspace serves any sequence of calls.
-constexpr size_t kWsCounters = 65536;
-constexpr size_t kWsScratch = kWsCounters * sizeof(uint32_t);
 
 // ---------------------------------------------------------------------------
 // Host-side error plumbing: a thread-local message, an int status code.
@@ -41,6 +36,9 @@ int hip_status(hipError_t e, const char *what);
     } while (0)
 
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// The vector-ALU product for m <= 4 rows (gemv.hip); arguments already checked.
+int gemv_launch(const ts_linear_args *a, void *stream);
 
 }  // namespace ts
 

@@ -1,4 +1,5 @@
 // "lanes": out[m, n] = after(sum_k x[m, k] w[n, k]) for m <= 16 rows.
+// Rows 1..4 go to the vector-ALU kernel in gemv.hip; 5..16 run here.
 //
 // Replaces the reference's few-row matmul rules: lanes (a 32-lane group per
 // column, engine/rules/linear/src/lanes.rs:17-143) and thin (a thread per
@@ -17,9 +18,9 @@
 // lo = bf16(x - hi)); hi*w + lo*w carries 16 mantissa bits of x, so f32 rows
 // times bf16 weights stay close to the f32 oracle. e4m3 weights decode to bf16
 // in registers; the per-row scale multiplies the finished sum.
-// k is split across the waves of a group (reduced in LDS) and across groups
-// (partials in the workspace; the last group to finish sums them in split
-// order, so results are deterministic).
+// k is split across the waves of a group and reduced in LDS; nothing crosses
+// groups (a device-wide fence to hand partials between groups costs more than
+// the whole product here), so results are deterministic.
 #include "common.h"
 
 #include <algorithm>
@@ -36,8 +37,6 @@ struct LanesParams {
     const float *gain;
     const float *a0;
     void *out;
-    float *partials;     // [splits][tiles][2][256]
-    uint32_t *counters;  // [tiles]
     uint32_t m, n, k;
     uint32_t stages;
     float eps;
@@ -175,14 +174,13 @@ TS_DEV float silu(float v) { return v / (1.0f + expf(-v)); }
 template <bool XF32, bool W8, bool SILU, bool NORM>
 __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t tile = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    const uint32_t tile = blockIdx.x, split = 0, splits = 1;
     const uint32_t col = lane & 15, grp = lane >> 4;
     const uint32_t n0 = tile * 16, M = p.m, N = p.n, K = p.k;
 
     __shared__ float red[kWaves][SILU ? 2 : 1][256];
     __shared__ float inv_s[16];
     __shared__ float part_s[kWaves][16];
-    __shared__ uint32_t last_s;
 
     // Fused RmsNorm prologue: every group computes the same inverse roots
     // (fixed reduction order, so all groups agree bit for bit).
@@ -244,26 +242,6 @@ __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p) {
         g += red[w][0][t];
         if (SILU) u += red[w][SILU ? 1 : 0][t];
     }
-    if (splits > 1) {
-        const uint32_t tiles = gridDim.x;
-        float *mine = p.partials + ((size_t)split * tiles + tile) * 512;
-        mine[t] = g;
-        if (SILU) mine[256 + t] = u;
-        __threadfence();
-        __syncthreads();
-        if (t == 0) last_s = atomicAdd(&p.counters[tile], 1u) == splits - 1;
-        __syncthreads();
-        if (!last_s) return;
-        __threadfence();
-        g = 0.0f; u = 0.0f;
-        for (uint32_t s = 0; s < splits; s++) {
-            const float *q = p.partials + ((size_t)s * tiles + tile) * 512;
-            g += __builtin_nontemporal_load(q + t);
-            if (SILU) u += __builtin_nontemporal_load(q + 256 + t);
-        }
-        if (t == 0) p.counters[tile] = 0;  // ready for the next launch
-    }
-
     const uint32_t m = t >> 4, n = n0 + (t & 15);
     if (m >= M || n >= N) return;
     if (W8) {
@@ -283,13 +261,7 @@ struct Plan {
 Plan plan(const ts_linear_args *a) {
     Plan pl;
     pl.tiles = (a->n + 15) / 16;
-    const uint32_t chunks = (a->k + kChunk - 1) / kChunk;
-    // Aim for ~2048 waves in flight; split k across groups only while each wave
-    // keeps at least one chunk.
-    uint32_t splits = 1;
-    while (pl.tiles * splits * 2 * kWaves <= 2048 && splits * 2 * kWaves <= chunks) splits *= 2;
-    if (pl.tiles > kWsCounters) splits = 1;
-    pl.splits = splits;
+    pl.splits = 1;
     return pl;
 }
 
@@ -321,10 +293,8 @@ int check(const ts_linear_args *a) {
 }  // namespace
 
 extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
-    if (!a) return 0;
-    Plan pl = plan(a);
-    if (pl.splits <= 1) return 0;
-    return kWsScratch + (size_t)pl.splits * pl.tiles * 512 * sizeof(float);
+    (void)a;
+    return 0;  // no entry point of this rule needs scratch
 }
 
 extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
@@ -335,20 +305,12 @@ extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.gain = a->gain; p.a0 = a->a0;
     p.out = a->out; p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.eps = a->eps;
     p.out_bf16 = a->out_dtype == TS_BF16;
-    p.partials = nullptr; p.counters = nullptr;
-    if (pl.splits > 1) {
-        size_t need = tessera_hip_lanes_workspace(a);
-        if (!a->workspace || a->workspace_bytes < need)
-            return ts::fail(TS_ERR_WORKSPACE, "lanes: workspace of %zu bytes needed, %zu given", need,
-                            a->workspace ? a->workspace_bytes : (size_t)0);
-        p.counters = (uint32_t *)a->workspace;
-        p.partials = (float *)((char *)a->workspace + kWsScratch);
-    }
+    if (a->m <= 4) return ts::gemv_launch(a, stream);
     const bool silu = a->stages & TS_AFTER_SILU_MUL, norm = a->stages & TS_BEFORE_RMS_NORM;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
     Kern k = xf ? (w8 ? pick2<true, true>(silu, norm) : pick2<true, false>(silu, norm))
                 : (w8 ? pick2<false, true>(silu, norm) : pick2<false, false>(silu, norm));
-    hipLaunchKernelGGL(k, dim3(pl.tiles, pl.splits), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(k, dim3(pl.tiles), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("lanes launch");
     return TS_OK;
 }

@@ -280,7 +280,7 @@ extern "C" int tessera_hip_gather(const void *table, const uint32_t *ids, float 
 
 extern "C" size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width) {
     const size_t spans = (width + kSpan - 1) / kSpan;
-    return kWsScratch + (size_t)rows * spans * (sizeof(float) + sizeof(uint32_t));
+    return (size_t)rows * spans * (sizeof(float) + sizeof(uint32_t));
 }
 
 extern "C" int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, uint32_t width, void *workspace,
@@ -293,7 +293,7 @@ extern "C" int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, 
     if (!workspace || workspace_bytes < need)
         return ts::fail(TS_ERR_WORKSPACE, "argmax: workspace of %zu bytes needed", need);
     const uint32_t spans = (width + kSpan - 1) / kSpan;
-    float *vals = (float *)((char *)workspace + kWsScratch);
+    float *vals = (float *)workspace;
     uint32_t *idx = (uint32_t *)((char *)vals + (size_t)rows * spans * sizeof(float));
     hipLaunchKernelGGL(argmax_spans, dim3(spans, rows), dim3(256), 0, (hipStream_t)stream, x, vals, idx, rows,
                        width, spans);

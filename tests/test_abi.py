@@ -47,6 +47,10 @@ def test_workspace_sizes():
     lib = abi.load()
     a = abi.LinearArgs()
     a.m, a.n, a.k = 1, 1024, 3072
-    assert lib.tessera_hip_lanes_workspace(C.byref(a)) > 0  # few tiles: split-K
-    a.n = 151936
-    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0  # nothing crosses groups
+    r = abi.RowsArgs()
+    r.rows, r.heads, r.kv_heads, r.width = 32, 16, 8, 128
+    r.max_position = 150
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 0  # one group per (row, kv head)
+    r.max_position = 8191
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 8 * 2 * 130 * 4
