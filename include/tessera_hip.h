@@ -133,6 +133,19 @@ typedef struct {
 int tessera_hip_attend_rows(const ts_rows_args *a, void *stream);
 size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
 
+/* The decode step of a Qwen3 layer in one launch: per-head RmsNorm (q_gain /
+ * k_gain, eps) and Halves RoPE (theta) of q and of the new k from the raw q/k/v
+ * product rows qkv [rows, (heads + 2*kv_heads) * width] f32; the new k and v rows
+ * written (bf16) into the kept rows at (slot, position) (a->k and a->v are
+ * written); then attend_rows over the kept rows, the new row included. a->q is
+ * ignored. Same split and workspace as tessera_hip_attend_rows. Every row must
+ * read only keys kept by earlier launches plus its own: rows of one launch may not
+ * share a slot (the decode shape: one new row per slot).
+ * Replaces: the q_norm/k_norm RmsNorm + rope + Append + attend_rows chain of
+ * engine/models/src/shared.rs:109-145 and engine/ir/interp/src/run.rs:122-198. */
+int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
+                            const float *k_gain, float eps, float theta, void *stream);
+
 /* Prefill: 64-row query blocks of one slot on the matrix unit, keys streamed
  * page by page with online softmax.
  * Replaces: rule "flash" / flash_rows (engine/rules/attention/src/flash.rs:416-503,

@@ -71,6 +71,7 @@ SIGNATURES = {
     "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
     "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),
+    "tessera_hip_attend_step": (C.c_int, [_RA, _P, _P, _P, C.c_float, C.c_float, _P]),
     "tessera_hip_rms_norm": (C.c_int, [_P, _P, _P, _U, _U, C.c_float, _P]),
     "tessera_hip_rope": (C.c_int, [_P, _P, _U, _U, _U, C.c_float, C.c_int32, _P]),
     "tessera_hip_qk_norm_rope_append": (C.c_int, [_P] * 9 + [_U] * 7 + [C.c_float, C.c_float, _P]),

@@ -24,6 +24,8 @@
 //    workspace and a second small kernel merges them in partition order. A
 //    kernel boundary orders the two: a device-wide fence inside one kernel costs
 //    more than the merge launch.
+#include <string.h>
+
 #include "common.h"
 
 namespace {
@@ -40,6 +42,10 @@ struct RowsParams {
     uint32_t rows, keys, heads, kv_heads, G, back, kept_pages, page_shift;
     uint32_t wave_keys;  // keys per wave per partition (multiple of 16)
     float scale;
+    // The fused decode step: raw q/k/v product rows, per-head gains, RoPE.
+    const float *qkv;
+    const float *q_gain, *k_gain;
+    float eps, theta;
 };
 
 TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
@@ -48,7 +54,21 @@ TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
     return ((uint64_t)p.table[entry] << p.page_shift) | (pos & ((1u << p.page_shift) - 1));
 }
 
-template <int G>
+// RmsNorm over one 128-wide head held as (d, d+64) in lane d of a wave, then
+// the Halves rotation of that pair (engine/ir/interp/src/cpu.rs:36-47, 371-377).
+TS_DEV void norm_rope(float &a, float &b, const float *g, uint32_t lane, uint32_t pos, float eps, float theta) {
+    const float s = wave_sum(a * a + b * b);
+    const float inv = 1.0f / sqrtf(s / 128.0f + eps);
+    a = a * (inv * g[lane]);
+    b = b * (inv * g[lane + 64]);
+    float sn, cs;
+    sincosf((float)pos * powf(theta, -((float)(2 * lane)) / 128.0f), &sn, &cs);
+    const float ra = a * cs - b * sn, rb = a * sn + b * cs;
+    a = ra;
+    b = rb;
+}
+
+template <int G, bool STEP>
 __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams p) {
     constexpr int kWaves = (64 / G) < kMaxWaves ? (64 / G) : kMaxWaves;  // LDS bound: waves x G <= 64
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
@@ -59,15 +79,53 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
     __shared__ float salpha[kWaves][G];
     __shared__ float sm[kWaves][G], sl[kWaves][G];
     __shared__ float so[kWaves][G][128];
+    __shared__ __attribute__((aligned(16))) float sq[STEP ? G : 1][128];          // fused step: q heads
+    __shared__ __attribute__((aligned(16))) uint16_t snew[STEP ? 2 : 1][128];     // fused step: new k, v
 
     const uint32_t pos = p.positions[r], slot = p.slots[r];
     const uint32_t from = pos > p.back ? pos - p.back : 0;
+
+    if (STEP) {
+        // Items: q heads kvh*G + 0..G-1, then the new k row, then the new v row;
+        // waves take them in turn. The raw rows come from the q/k/v product.
+        const size_t base = (size_t)r * (p.heads + 2 * p.kv_heads) * 128;
+        for (uint32_t it = wave; it < (uint32_t)G + 2; it += waves) {
+            if (it < (uint32_t)G) {
+                const float *src = p.qkv + base + (size_t)(kvh * G + it) * 128;
+                float a = src[lane], b = src[lane + 64];
+                norm_rope(a, b, p.q_gain, lane, pos, p.eps, p.theta);
+                sq[it][lane] = a;
+                sq[it][lane + 64] = b;
+            } else if (it == (uint32_t)G) {
+                const float *src = p.qkv + base + (size_t)(p.heads + kvh) * 128;
+                float a = src[lane], b = src[lane + 64];
+                norm_rope(a, b, p.k_gain, lane, pos, p.eps, p.theta);
+                snew[0][lane] = bf16_bits(a);
+                snew[0][lane + 64] = bf16_bits(b);
+            } else {
+                const float *src = p.qkv + base + (size_t)(p.heads + p.kv_heads + kvh) * 128;
+                snew[1][lane] = bf16_bits(src[lane]);
+                snew[1][lane + 64] = bf16_bits(src[lane + 64]);
+            }
+        }
+        __syncthreads();
+        if (part == 0) {
+            // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198).
+            const uint64_t row = kept_row(p, slot, pos);
+            for (uint32_t i = threadIdx.x; i < 128; i += blockDim.x) {
+                const uint32_t which = i >> 6;
+                uint16_t *dst = (uint16_t *)(which == 0 ? p.k : p.v) + (row * p.kv_heads + kvh) * 128;
+                ((uint32_t *)dst)[i & 63] = ((const uint32_t *)snew[which])[i & 63];
+            }
+        }
+    }
 
     // q operand: row (head) col of the group, d-group grp; two bf16 parts.
     u32x4 qh[4], ql[4];
     {
         const bool ok = col < G;
-        const float *qr = p.q + ((size_t)r * p.heads + kvh * G + (ok ? col : 0)) * 128 + 32 * grp;
+        const float *qr = STEP ? &sq[ok ? col : 0][32 * grp]
+                               : p.q + ((size_t)r * p.heads + kvh * G + (ok ? col : 0)) * 128 + 32 * grp;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t h[4], l[4];
@@ -97,6 +155,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
     for (uint32_t b = 0; b < blocks; b++) {
         const uint32_t kb = wk0 + 16 * b;
         const bool live = kb <= pos && kb + 16 > from;  // uniform across the wave
+        uint32_t vv[16];
         if (live) {
             const uint64_t row0 = kept_row(p, slot, kb);  // 16 rows of one page
             const uint32_t key = kb + col;
@@ -104,8 +163,23 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
             // Dense kept rows end at the slot's capacity; pages always hold whole blocks.
             const bool in_mem = p.table || key < p.keys;
             u32x4 kk[4];
+            if (STEP && key == pos) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) kk[j] = in_mem ? *((const u32x4 *)kr + j) : u32x4{0, 0, 0, 0};
+                for (int j = 0; j < 4; j++) kk[j] = *((const u32x4 *)&snew[0][32 * grp] + j);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) kk[j] = in_mem ? *((const u32x4 *)kr + j) : u32x4{0, 0, 0, 0};
+            }
+            // V rows of the block, issued with K: lane owns dims 2*lane, 2*lane+1.
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const uint32_t kpos = kb + i;
+                vv[i] = 0;
+                if (kpos >= from && kpos <= pos) {
+                    if (STEP && kpos == pos) vv[i] = ((const uint32_t *)snew[1])[lane];
+                    else vv[i] = *((const uint32_t *)(p.v + ((row0 + i) * p.kv_heads + kvh) * 128) + lane);
+                }
+            }
             f32x4 s = {0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -142,15 +216,12 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
                 o0[h] *= a;
                 o1[h] *= a;
             }
-            const uint32_t kmax = min(kb + 16, pos + 1);
-            const uint64_t row0 = kept_row(p, slot, kb);
-            for (uint32_t key = max(kb, from); key < kmax; key++) {
-                const uint32_t i = key - kb;
-                const uint32_t vv = *((const uint32_t *)(p.v + ((row0 + i) * p.kv_heads + kvh) * 128) + lane);
-                const float v0 = lo_bf16(vv), v1 = hi_bf16(vv);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float v0 = lo_bf16(vv[i]), v1 = hi_bf16(vv[i]);
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    const float pk = sp[wave][i][h];
+                    const float pk = sp[wave][i][h];  // zero for keys outside [from, pos]
                     o0[h] += pk * v0;
                     o1[h] += pk * v1;
                 }
@@ -264,12 +335,11 @@ extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
     return groups * s.parts * G * 130 * sizeof(float);
 }
 
-extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
-    int rc = check(a);
-    if (rc) return rc;
-    if (a->rows == 0) return TS_OK;
+namespace {
+
+template <bool STEP>
+int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     Split s = split(a);
-    RowsParams p;
     p.q = (const float *)a->q; p.k = (const uint16_t *)a->k; p.v = (const uint16_t *)a->v;
     p.out = (float *)a->out; p.slots = a->slots; p.positions = a->positions; p.table = a->kept_table;
     p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads;
@@ -286,11 +356,11 @@ extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
     void (*k)(RowsParams) = nullptr;
     void (*merge)(RowsParams, uint32_t) = nullptr;
     switch (p.G) {
-    case 1: k = attend_rows_kernel<1>; merge = attend_rows_merge<1>; break;
-    case 2: k = attend_rows_kernel<2>; merge = attend_rows_merge<2>; break;
-    case 4: k = attend_rows_kernel<4>; merge = attend_rows_merge<4>; break;
-    case 8: k = attend_rows_kernel<8>; merge = attend_rows_merge<8>; break;
-    case 16: k = attend_rows_kernel<16>; merge = attend_rows_merge<16>; break;
+    case 1: k = attend_rows_kernel<1, STEP>; merge = attend_rows_merge<1>; break;
+    case 2: k = attend_rows_kernel<2, STEP>; merge = attend_rows_merge<2>; break;
+    case 4: k = attend_rows_kernel<4, STEP>; merge = attend_rows_merge<4>; break;
+    case 8: k = attend_rows_kernel<8, STEP>; merge = attend_rows_merge<8>; break;
+    case 16: k = attend_rows_kernel<16, STEP>; merge = attend_rows_merge<16>; break;
     default: return ts::fail(TS_ERR_ARG, "attend_rows: %u query heads per kv head (1, 2, 4, 8 or 16)", p.G);
     }
     hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(s.waves * 64), 0, (hipStream_t)stream, p);
@@ -300,4 +370,29 @@ extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
         TS_CHECK_LAUNCH("attend_rows merge launch");
     }
     return TS_OK;
+}
+
+}  // namespace
+
+extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
+    int rc = check(a);
+    if (rc) return rc;
+    if (a->rows == 0) return TS_OK;
+    RowsParams p;
+    memset(&p, 0, sizeof p);
+    return launch_rows<false>(a, p, stream);
+}
+
+extern "C" int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
+                                       const float *k_gain, float eps, float theta, void *stream) {
+    TS_REQUIRE(a && qkv && q_gain && k_gain, "attend_step: null pointer");
+    ts_rows_args b = *a;
+    b.q = qkv;  // q comes from the product rows; only checked for alignment
+    int rc = check(&b);
+    if (rc) return rc;
+    if (a->rows == 0) return TS_OK;
+    RowsParams p;
+    memset(&p, 0, sizeof p);
+    p.qkv = qkv; p.q_gain = q_gain; p.k_gain = k_gain; p.eps = eps; p.theta = theta;
+    return launch_rows<true>(&b, p, stream);
 }

@@ -20,6 +20,9 @@
 //  * waves reduce with butterflies, groups with one LDS exchange; nothing crosses
 //    groups, so there are no fences, atomics or workspace, and results are
 //    deterministic.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace ts {
@@ -87,6 +90,20 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
     const uint32_t ke = min(K, kb + s_per * STEP);
     const bool vec = (K % E) == 0;  // 16-byte aligned rows
 
+    // Epilogue operands of the output this lane may finish (wave 0, lane < outs*M),
+    // fetched now so their latency hides under the weight stream.
+    float pre_a0 = 0.0f, pre_sg = 1.0f, pre_su = 1.0f;
+    {
+        const uint32_t o = lane / M, m = lane % M, n = o0 + o;
+        if (wave == 0 && lane < outs * M && m < Mr && n < N) {
+            if (p.stages & TS_AFTER_ADD) pre_a0 = p.a0[(size_t)m * N + n];
+            if (W8) {
+                pre_sg = bf16_float(p.w_scale[n]);
+                if (silu) pre_su = bf16_float(p.w_scale[N + n]);
+            }
+        }
+    }
+
     float acc[R][M];
     float ssq[M];
 #pragma unroll
@@ -99,6 +116,7 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
     for (uint32_t k0 = kb; k0 < ke; k0 += B * STEP) {
         u32x4 wv[B][R];
         float xv[B][M][E];
+        float gv[B][E];
         // Issue every load of the batch first.
 #pragma unroll
         for (int b = 0; b < B; b++) {
@@ -119,6 +137,18 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
                     wv[b][r] = u32x4{t[0], t[1], t[2], t[3]};
                 } else {
                     wv[b][r] = u32x4{0, 0, 0, 0};
+                }
+            }
+            if (norm) {
+                if (full) {
+#pragma unroll
+                    for (int q = 0; q < E / 4; q++) {
+                        const float4 t = ((const float4 *)(p.gain + kk))[q];
+                        gv[b][4 * q] = t.x; gv[b][4 * q + 1] = t.y; gv[b][4 * q + 2] = t.z; gv[b][4 * q + 3] = t.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < E; e++) gv[b][e] = kk + e < ke ? p.gain[kk + e] : 0.0f;
                 }
             }
 #pragma unroll
@@ -159,25 +189,13 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
         // Then use them: RmsNorm's sum of squares, the gain, the dots.
 #pragma unroll
         for (int b = 0; b < B; b++) {
-            const uint32_t kk = k0 + b * STEP + lane * E;
             if (norm) {
-                float g[E];
-                if (vec && kk + E <= ke) {
-#pragma unroll
-                    for (int q = 0; q < E / 4; q++) {
-                        const float4 t = ((const float4 *)(p.gain + kk))[q];
-                        g[4 * q] = t.x; g[4 * q + 1] = t.y; g[4 * q + 2] = t.z; g[4 * q + 3] = t.w;
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < E; e++) g[e] = kk + e < ke ? p.gain[kk + e] : 0.0f;
-                }
 #pragma unroll
                 for (int m = 0; m < M; m++)
 #pragma unroll
                     for (int e = 0; e < E; e++) {
                         ssq[m] += xv[b][m][e] * xv[b][m][e];
-                        xv[b][m][e] *= g[e];
+                        xv[b][m][e] *= gv[b][e];
                     }
             }
 #pragma unroll
@@ -251,11 +269,11 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
         u *= inv;
     }
     if (W8) {
-        g *= bf16_float(p.w_scale[n]);
-        if (silu) u *= bf16_float(p.w_scale[N + n]);
+        g *= pre_sg;
+        u *= pre_su;
     }
     float v = silu ? g / (1.0f + expf(-g)) * u : g;
-    if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
+    if (p.stages & TS_AFTER_ADD) v += pre_a0;
     if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
     else ((float *)p.out)[(size_t)m * N + n] = v;
 }
@@ -283,18 +301,31 @@ Kern pick_m(uint32_t m, int r) {
 // Rows per group and waves per group for a product shape: enough waves to
 // cover the chip (~2048), whole k steps per wave.
 void gemv_plan(uint32_t n, uint32_t k, bool silu, bool w8, int *rows, uint32_t *waves, uint32_t *groups) {
+    // TESSERA_GEMV_PLAN="rows,waves" pins the choice (for tuning sweeps).
+    static const char *pin = getenv("TESSERA_GEMV_PLAN");
+    if (pin) {
+        int r = 0, w = 0;
+        if (sscanf(pin, "%d,%d", &r, &w) == 2 && (r == 2 || r == 4 || r == 8) && w >= 1 && w <= 4) {
+            const uint32_t outs = silu ? r / 2 : r;
+            *rows = r;
+            *waves = (uint32_t)w;
+            *groups = (n + outs - 1) / outs;
+            return;
+        }
+    }
+    // Measured on MI355X (graph-replayed, cold weights): one wave per group is
+    // fastest at every decode shape (an LDS exchange costs more than it saves),
+    // and rows per wave grow with the row count: 8 for >= 3072 rows of 1024,
+    // 4 for ~1024 rows of 2048, 2 for ~1024 rows of 3072.
+    (void)w8;
     const uint32_t total = silu ? 2 * n : n;
-    int r = 2;
-    if (total / 8 >= 2048) r = 8;
-    else if (total / 4 >= 1024) r = 4;
+    int r;
+    if (total >= 3072) r = 8;
+    else if (k <= 2048) r = 4;
+    else r = 2;
     const uint32_t outs = silu ? r / 2 : r;
     const uint32_t g = (n + outs - 1) / outs;
-    const uint32_t step = w8 ? 1024 : 512;
-    const uint32_t steps = (k + step - 1) / step;
-    uint32_t w = 1;
-    if (g < 2048)
-        for (uint32_t c = 4; c >= 2; c--)
-            if (steps % c == 0) { w = c; break; }
+    const uint32_t w = 1;
     *rows = r;
     *waves = w;
     *groups = g;

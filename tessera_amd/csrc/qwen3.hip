@@ -166,11 +166,17 @@ int run_layers(ts_qwen3 *m, uint32_t rows, const uint32_t *slots, const uint32_t
             TRY(tessera_hip_rms_norm(m->x, L.ln1, m->xn, rows, H, c.eps, s));
         }
         TRY(tessera_hip_linear(&a, s));
-        TRY(tessera_hip_qk_norm_rope_append(m->qkv, L.q_norm, L.k_norm, m->q, L.k_cache, L.v_cache, slots, pos,
-                                            m->d_table, rows, c.heads, c.kv_heads, D, m->kept_pages * c.page,
-                                            m->kept_pages, c.page, c.eps, c.theta, s));
         ts_rows_args r = rows_args(m, L, rows, slots, pos, max_position);
-        TRY(fused ? tessera_hip_attend_rows(&r, s) : tessera_hip_flash_rows(&r, s));
+        if (rows == 1) {
+            // q/k norm, RoPE, the kept-row append and attention in one launch (a row
+            // may only read keys appended by earlier launches, so one row per slot).
+            TRY(tessera_hip_attend_step(&r, m->qkv, L.q_norm, L.k_norm, c.eps, c.theta, s));
+        } else {
+            TRY(tessera_hip_qk_norm_rope_append(m->qkv, L.q_norm, L.k_norm, m->q, L.k_cache, L.v_cache, slots,
+                                                pos, m->d_table, rows, c.heads, c.kv_heads, D,
+                                                m->kept_pages * c.page, m->kept_pages, c.page, c.eps, c.theta, s));
+            TRY(fused ? tessera_hip_attend_rows(&r, s) : tessera_hip_flash_rows(&r, s));
+        }
         a = lin(m->attn, L.o, m->x, rows, H, QD, m);
         a.stages = TS_AFTER_ADD;
         a.a0 = m->x;

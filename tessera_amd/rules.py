@@ -126,6 +126,22 @@ def attend_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_page
     return out
 
 
+def attend_step(qkv, q_gain, k_gain, k, v, slots, positions, *, heads, keys, scale, eps, theta, table=None,
+                kept_pages=0, page=16, back=abi.U32_MAX, max_position=None, out=None):
+    """Fused decode step: q/k RmsNorm + RoPE from raw product rows, append, attend."""
+    rows = qkv.shape[0]
+    if out is None:
+        out = torch.empty((rows, heads, 128), dtype=torch.float32, device=qkv.device)
+    qshape = torch.empty((rows, heads, 128), device=qkv.device)  # shape carrier only
+    a = rows_args(qshape, k, v, out, slots, positions, keys=keys, scale=scale, table=table,
+                  kept_pages=kept_pages, page=page, back=back, max_position=max_position)
+    need = abi.load().tessera_hip_attend_rows_workspace(C.byref(a))
+    a.workspace, a.workspace_bytes = workspace(qkv.device).get(need)
+    abi.call("tessera_hip_attend_step", C.byref(a), _ptr(qkv), _ptr(q_gain), _ptr(k_gain), C.c_float(eps),
+             C.c_float(theta), _stream())
+    return out
+
+
 def flash_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
                back=abi.U32_MAX, out=None):
     """Prefill rows over kept K/V (rule "flash"/flash_rows)."""

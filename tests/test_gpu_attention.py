@@ -106,3 +106,37 @@ def test_prefill_flash_rows(lens):
 def test_prefill_flash_window_and_gqa():
     c = paged_case(8, [200], heads=8, kv_heads=2, pos=([0] * 200, list(range(200))))
     np.testing.assert_allclose(run("flash", c, 0.25, back=40), want(c, 0.25, "back", 40), atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("ctx", [1, 16, 17, 150, 3000])
+def test_attend_step_fused(ctx):
+    """q/k RmsNorm + Halves RoPE + append + attend in one launch, against the oracle's
+    chain (rms_norm per head, rope, bf16 kept rows, attend_rows)."""
+    from tessera_amd import rules as R
+    c = paged_case(ctx, [ctx], pos=([0], [ctx - 1]))
+    r = rng(ctx + 5)
+    heads, kvh = 16, 8
+    qkv = r.standard_normal((1, (heads + 2 * kvh) * 128)).astype(np.float32)
+    qg = (1 + 0.05 * r.standard_normal(128)).astype(np.float32)
+    kg = (1 + 0.05 * r.standard_normal(128)).astype(np.float32)
+    kd, vd = to_dev(c["kb"], torch), to_dev(c["vb"], torch)
+    s = 1 / math.sqrt(128)
+    got = from_dev(R.attend_step(to_dev(qkv, torch), to_dev(qg, torch), to_dev(kg, torch), kd, vd,
+                                 to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                                 heads=heads, keys=c["keys"], scale=s, eps=1e-6, theta=1e6,
+                                 table=to_dev(c["table"], torch, torch.int32), kept_pages=c["kept_pages"],
+                                 page=c["page"]))
+    pos = np.array([ctx - 1], np.uint32)
+    q = O.rope(O.rms_norm(qkv[:, : heads * 128].reshape(1, heads, 128), qg, 1e-6), pos, 1e6)
+    k = O.rope(O.rms_norm(qkv[:, heads * 128:(heads + kvh) * 128].reshape(1, kvh, 128), kg, 1e-6), pos, 1e6)
+    v = qkv[:, (heads + kvh) * 128:].reshape(1, kvh, 128)
+    row = O.paged_row(c["table"], c["kept_pages"], c["page"], 0, ctx - 1)
+    kf, vf = c["kf"].copy(), c["vf"].copy()
+    kf[row], vf[row] = O.bf16_round(k[0]), O.bf16_round(v[0])
+    want = O.attend_rows(q, kf, vf, [0], pos, c["keys"], s, table=c["table"], kept_pages=c["kept_pages"],
+                         page=c["page"])
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=0)
+    # The new rows landed in the kept rows, bf16: v exactly, k within one bf16 step
+    # (device powf/sincosf against the host's for the rotation angle).
+    assert np.array_equal(from_dev(vd)[row], vf[row])
+    np.testing.assert_allclose(from_dev(kd)[row], kf[row], rtol=2 ** -7, atol=1e-6)
