@@ -41,6 +41,9 @@ def parse():
     p.add_argument("--cpu-steps", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-gemm", action="store_true")
+    p.add_argument("--roofline-only", action="store_true",
+                   help="run only the lm_head lanes kernel and a plain copy of known size "
+                        "(the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
     return p.parse_args()
 
 
@@ -68,6 +71,17 @@ def lm_head_roofline(torch, reps=20):
     return {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": nbytes / t / HBM_PEAK, "traffic": None, "kernel": "lanes_kernel (lm_head 151936x1024)",
             "bytes_per_launch": nbytes, "us_per_launch": t * 1e6}
+
+
+def copy_reference(torch, nbytes=256 << 20, reps=5):
+    """A plain device copy of known size: the yardstick that scales FETCH_SIZE and
+    WRITE_SIZE counters to bytes."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
 
 
 def gemm_sweep(torch, reps=10):
@@ -138,6 +152,11 @@ def main():
     import numpy as np
     import torch
 
+    if a.roofline_only:
+        roof = lm_head_roofline(torch, reps=5)
+        copy_reference(torch)
+        print(json.dumps({"roofline": roof}), flush=True)
+        return
     from tessera_amd.qwen3 import Qwen3, default_config
     cfg = default_config(max_context=PROMPT + max(a.steps, a.warmup) + 1, max_prompt=PROMPT)
     m = Qwen3(cfg, seed=0)

@@ -134,7 +134,8 @@ int tessera_hip_attend_rows(const ts_rows_args *a, void *stream);
 size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
 
 /* The decode step of a Qwen3 layer in one launch: per-head RmsNorm (q_gain /
- * k_gain, eps) and Halves RoPE (theta) of q and of the new k from the raw q/k/v
+ * k_gain, eps) and Halves RoPE (angles from rope_table, rows >= max_position + 1,
+ * as tessera_hip_rope_table fills it) of q and of the new k from the raw q/k/v
  * product rows qkv [rows, (heads + 2*kv_heads) * width] f32; the new k and v rows
  * written (bf16) into the kept rows at (slot, position) (a->k and a->v are
  * written); then attend_rows over the kept rows, the new row included. a->q is
@@ -144,7 +145,8 @@ size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
  * Replaces: the q_norm/k_norm RmsNorm + rope + Append + attend_rows chain of
  * engine/models/src/shared.rs:109-145 and engine/ir/interp/src/run.rs:122-198. */
 int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
-                            const float *k_gain, float eps, float theta, void *stream);
+                            const float *k_gain, const float *rope_table, uint32_t rope_rows, float eps,
+                            void *stream);
 
 /* Prefill: 64-row query blocks of one slot on the matrix unit, keys streamed
  * page by page with online softmax.
@@ -168,6 +170,11 @@ int tessera_hip_rms_norm(const float *x, const float *gain, float *out, uint32_t
  * Replaces: "angles" + "rope" (engine/rules/kernels/src/rope.rs:10-125). */
 int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t rows, uint32_t heads,
                      uint32_t width, float theta, int32_t halves, void *stream);
+
+/* The angle table: table[(pos * width/2 + j) * 2 + {0, 1}] = (cos, sin) of
+ * pos * theta^(-2j/width) for pos < positions, j < width/2.
+ * Replaces: the "angles" stage (engine/rules/kernels/src/rope.rs:10-58). */
+int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t width, float theta, void *stream);
 
 /* The step between the q/k/v product and attention for a Qwen3 layer: per head
  * RmsNorm (q_gain / k_gain, eps) then Halves RoPE on q and k, then the new k

@@ -12,7 +12,7 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libtessera_hip.so")
+LIB_PATH = os.environ.get("TESSERA_HIP_LIB") or os.path.join(HERE, "libtessera_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "tessera_hip.h")
 
 TS_OK = 0
@@ -71,7 +71,8 @@ SIGNATURES = {
     "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
     "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),
-    "tessera_hip_attend_step": (C.c_int, [_RA, _P, _P, _P, C.c_float, C.c_float, _P]),
+    "tessera_hip_attend_step": (C.c_int, [_RA, _P, _P, _P, _P, _U, C.c_float, _P]),
+    "tessera_hip_rope_table": (C.c_int, [_P, _U, _U, C.c_float, _P]),
     "tessera_hip_rms_norm": (C.c_int, [_P, _P, _P, _U, _U, C.c_float, _P]),
     "tessera_hip_rope": (C.c_int, [_P, _P, _U, _U, _U, C.c_float, C.c_int32, _P]),
     "tessera_hip_qk_norm_rope_append": (C.c_int, [_P] * 9 + [_U] * 7 + [C.c_float, C.c_float, _P]),

@@ -16,6 +16,11 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libtessera_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# Extra device flags (e.g. -DTS_MARKS for an in-kernel mark build) and output path.
+EXTRA = os.environ.get("TESSERA_HIP_CFLAGS", "").split()
+if os.environ.get("TESSERA_HIP_OUT"):
+    LIB = os.path.abspath(os.environ["TESSERA_HIP_OUT"])
+    OBJ = LIB + ".objs"
 
 # -packed-fp32-ops off: packed f32 VALU forms are not used on this pool.
 DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-munsafe-fp-atomics",
@@ -25,7 +30,7 @@ DEVICE_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-munsafe
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *DEVICE_FLAGS, *EXTRA, "-c", src, "-o", obj]
     if src.endswith(".cpp"):
         cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

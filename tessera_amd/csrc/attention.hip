@@ -18,7 +18,7 @@
 //  * Online softmax per head in registers (16-lane butterflies), then P*V on
 //    the vector ALUs: a lane owns 2 adjacent head dims, so each V row is one
 //    256-byte coalesced load across the wave.
-//  * A group's waves (up to 16) split its keys and merge (max, sum, acc) in LDS.
+//  * A group's waves (up to 8) split its keys and merge (max, sum, acc) in LDS.
 //    Short contexts (the batch-1 decode) take one group per (row, kv head).
 //    Long ones split keys across groups too: each writes its partial to the
 //    workspace and a second small kernel merges them in partition order. A
@@ -28,9 +28,23 @@
 
 #include "common.h"
 
+#ifdef TS_MARKS
+// Debug builds: a device ledger for TS_MARK, read back by tessera_hip_debug_marks.
+static uint64_t *ts_debug_marks() {
+    static uint64_t *ledger = nullptr;
+    if (!ledger && hipMalloc((void **)&ledger, 16 * 65536 * sizeof(uint64_t)) != hipSuccess) ledger = nullptr;
+    return ledger;
+}
+extern "C" int tessera_hip_debug_marks(uint64_t *host, uint32_t count) {
+    uint64_t *d = ts_debug_marks();
+    if (!d) return -1;
+    return hipMemcpy(host, d, count * sizeof(uint64_t), hipMemcpyDeviceToHost) == hipSuccess ? 0 : -1;
+}
+#endif
+
 namespace {
 
-constexpr int kMaxWaves = 16;
+constexpr int kMaxWaves = 8;  // 512 threads: room for two blocks of K/V in registers
 constexpr int kMaxG = 16;
 
 struct RowsParams {
@@ -45,7 +59,9 @@ struct RowsParams {
     // The fused decode step: raw q/k/v product rows, per-head gains, RoPE.
     const float *qkv;
     const float *q_gain, *k_gain;
-    float eps, theta;
+    const float *rope;  // [positions][64] (cos, sin) pairs
+    float eps;
+    uint64_t *marks;    // TS_MARK ledger (debug builds)
 };
 
 TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
@@ -55,20 +71,20 @@ TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
 }
 
 // RmsNorm over one 128-wide head held as (d, d+64) in lane d of a wave, then
-// the Halves rotation of that pair (engine/ir/interp/src/cpu.rs:36-47, 371-377).
-TS_DEV void norm_rope(float &a, float &b, const float *g, uint32_t lane, uint32_t pos, float eps, float theta) {
+// the Halves rotation of that pair by the tabled angle (engine/ir/interp/src/
+// cpu.rs:36-47, 371-377; the table is the reference's `angles` stage,
+// engine/rules/kernels/src/rope.rs:10-58).
+TS_DEV void norm_rope(float &a, float &b, float ga, float gb, float cs, float sn, float eps) {
     const float s = wave_sum(a * a + b * b);
     const float inv = 1.0f / sqrtf(s / 128.0f + eps);
-    a = a * (inv * g[lane]);
-    b = b * (inv * g[lane + 64]);
-    float sn, cs;
-    sincosf((float)pos * powf(theta, -((float)(2 * lane)) / 128.0f), &sn, &cs);
+    a = a * (inv * ga);
+    b = b * (inv * gb);
     const float ra = a * cs - b * sn, rb = a * sn + b * cs;
     a = ra;
     b = rb;
 }
 
-template <int G, bool STEP>
+template <int G, bool STEP, int NB>
 __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams p) {
     constexpr int kWaves = (64 / G) < kMaxWaves ? (64 / G) : kMaxWaves;  // LDS bound: waves x G <= 64
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
@@ -76,39 +92,94 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
     const uint32_t col = lane & 15, grp = lane >> 4;
 
     __shared__ float sp[kWaves][16][G];  // p[key][head] of the current block
-    __shared__ float salpha[kWaves][G];
     __shared__ float sm[kWaves][G], sl[kWaves][G];
     __shared__ float so[kWaves][G][128];
     __shared__ __attribute__((aligned(16))) float sq[STEP ? G : 1][128];          // fused step: q heads
     __shared__ __attribute__((aligned(16))) uint16_t snew[STEP ? 2 : 1][128];     // fused step: new k, v
 
+    TS_MARK(p.marks, 0);
     const uint32_t pos = p.positions[r], slot = p.slots[r];
     const uint32_t from = pos > p.back ? pos - p.back : 0;
+    const uint32_t wk0 = (part * waves + wave) * (16 * NB);
+    const uint32_t pmask = (1u << p.page_shift) - 1;
+
+    // Loads are issued in the order their values are needed, because the memory
+    // counter retires them in order: page-table entries, then the fused step's
+    // inputs, then this wave's K/V blocks. Every load is unconditional (addresses
+    // clamped to rows that exist, results masked later) so the compiler can wait
+    // for exactly the loads a value needs instead of all of them.
+    bool live[NB];
+    uint32_t kbc[NB], page_of[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        const uint32_t kb = wk0 + 16 * nb;
+        live[nb] = kb <= pos && kb + 16 > from;  // uniform across the wave
+        kbc[nb] = min(kb, pos) & ~15u;           // a 16-aligned block whose page exists
+        page_of[nb] = p.table ? p.table[(uint64_t)slot * p.kept_pages + (kbc[nb] >> p.page_shift)] : 0u;
+    }
+    // Fused step inputs: wave w < G + 2 takes item w (q heads, new k, new v); the
+    // host launches at least G + 2 waves whenever the LDS budget allows.
+    constexpr bool kOneItem = G + 2 <= kWaves;
+    const uint32_t item = min(wave, (uint32_t)G + 1);
+    const size_t qkv_base = (size_t)r * (p.heads + 2 * p.kv_heads) * 128;
+    float ra = 0.0f, rb = 0.0f, qga = 0.0f, qgb = 0.0f, kga = 0.0f, kgb = 0.0f;
+    float2 cs = make_float2(1.0f, 0.0f);
+    if (STEP) {
+        const uint32_t rowh = item < (uint32_t)G ? kvh * G + item
+                                                 : (item == (uint32_t)G ? p.heads + kvh : p.heads + p.kv_heads + kvh);
+        const float *src = p.qkv + qkv_base + (size_t)rowh * 128;
+        ra = src[lane];
+        rb = src[lane + 64];
+        cs = ((const float2 *)p.rope)[(size_t)pos * 64 + lane];
+        qga = p.q_gain[lane];
+        qgb = p.q_gain[lane + 64];
+        kga = p.k_gain[lane];
+        kgb = p.k_gain[lane + 64];
+    }
+    u32x4 kk[NB][4];
+    uint32_t vv[NB][16];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+        // 16 rows of one page (pages hold >= 16 rows); dense rows clamp at the
+        // slot's capacity. Rows outside [from, pos] are masked where they are used.
+        const uint64_t row0 = p.table ? (((uint64_t)page_of[nb] << p.page_shift) | (kbc[nb] & pmask))
+                                      : (uint64_t)slot * p.keys + kbc[nb];
+        const uint32_t room = p.table ? 15u : p.keys - 1 - min(kbc[nb], p.keys - 1);
+        const uint16_t *kr = p.k + ((row0 + min(col, room)) * p.kv_heads + kvh) * 128 + 32 * grp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) kk[nb][j] = *((const u32x4 *)kr + j);
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+            vv[nb][i] = *((const uint32_t *)(p.v + ((row0 + min((uint32_t)i, room)) * p.kv_heads + kvh) * 128) + lane);
+    }
 
     if (STEP) {
-        // Items: q heads kvh*G + 0..G-1, then the new k row, then the new v row;
-        // waves take them in turn. The raw rows come from the q/k/v product.
-        const size_t base = (size_t)r * (p.heads + 2 * p.kv_heads) * 128;
-        for (uint32_t it = wave; it < (uint32_t)G + 2; it += waves) {
+        for (uint32_t it = item; it < (uint32_t)G + 2; it += waves) {
+            if (!kOneItem && it != item) {  // fewer waves than items: later items load here
+                const uint32_t rowh = it < (uint32_t)G ? kvh * G + it
+                                                       : (it == (uint32_t)G ? p.heads + kvh : p.heads + p.kv_heads + kvh);
+                const float *src = p.qkv + qkv_base + (size_t)rowh * 128;
+                ra = src[lane];
+                rb = src[lane + 64];
+            }
+            if (it == item && wave > (uint32_t)G + 1) break;  // spare wave: no item of its own
+            float a = ra, b = rb;
             if (it < (uint32_t)G) {
-                const float *src = p.qkv + base + (size_t)(kvh * G + it) * 128;
-                float a = src[lane], b = src[lane + 64];
-                norm_rope(a, b, p.q_gain, lane, pos, p.eps, p.theta);
+                norm_rope(a, b, qga, qgb, cs.x, cs.y, p.eps);
                 sq[it][lane] = a;
                 sq[it][lane + 64] = b;
             } else if (it == (uint32_t)G) {
-                const float *src = p.qkv + base + (size_t)(p.heads + kvh) * 128;
-                float a = src[lane], b = src[lane + 64];
-                norm_rope(a, b, p.k_gain, lane, pos, p.eps, p.theta);
+                norm_rope(a, b, kga, kgb, cs.x, cs.y, p.eps);
                 snew[0][lane] = bf16_bits(a);
                 snew[0][lane + 64] = bf16_bits(b);
             } else {
-                const float *src = p.qkv + base + (size_t)(p.heads + p.kv_heads + kvh) * 128;
-                snew[1][lane] = bf16_bits(src[lane]);
-                snew[1][lane + 64] = bf16_bits(src[lane + 64]);
+                snew[1][lane] = bf16_bits(a);
+                snew[1][lane + 64] = bf16_bits(b);
             }
+            if (kOneItem) break;
         }
         __syncthreads();
+        TS_MARK(p.marks, 1);
         if (part == 0) {
             // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198).
             const uint64_t row = kept_row(p, slot, pos);
@@ -150,84 +221,58 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
 #pragma unroll
     for (int h = 0; h < G; h++) { o0[h] = 0.0f; o1[h] = 0.0f; }
 
-    const uint32_t wk0 = (part * waves + wave) * p.wave_keys;
-    const uint32_t blocks = p.wave_keys / 16;
-    for (uint32_t b = 0; b < blocks; b++) {
-        const uint32_t kb = wk0 + 16 * b;
-        const bool live = kb <= pos && kb + 16 > from;  // uniform across the wave
-        uint32_t vv[16];
-        if (live) {
-            const uint64_t row0 = kept_row(p, slot, kb);  // 16 rows of one page
-            const uint32_t key = kb + col;
-            const uint16_t *kr = p.k + ((row0 + col) * p.kv_heads + kvh) * 128 + 32 * grp;
-            // Dense kept rows end at the slot's capacity; pages always hold whole blocks.
-            const bool in_mem = p.table || key < p.keys;
-            u32x4 kk[4];
-            if (STEP && key == pos) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) kk[j] = *((const u32x4 *)&snew[0][32 * grp] + j);
-            } else {
+    for (int nb = 0; nb < NB; nb++) {
+        if (!live[nb]) continue;  // uniform across the wave
+        const uint32_t kb = wk0 + 16 * nb;
+        const uint32_t key = kb + col;
+        if (STEP && key == pos) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) kk[j] = in_mem ? *((const u32x4 *)kr + j) : u32x4{0, 0, 0, 0};
-            }
-            // V rows of the block, issued with K: lane owns dims 2*lane, 2*lane+1.
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const uint32_t kpos = kb + i;
-                vv[i] = 0;
-                if (kpos >= from && kpos <= pos) {
-                    if (STEP && kpos == pos) vv[i] = ((const uint32_t *)snew[1])[lane];
-                    else vv[i] = *((const uint32_t *)(p.v + ((row0 + i) * p.kv_heads + kvh) * 128) + lane);
-                }
-            }
-            f32x4 s = {0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                s = mfma16(as_bf16x8(qh[j]), as_bf16x8(kk[j]), s);
-                s = mfma16(as_bf16x8(ql[j]), as_bf16x8(kk[j]), s);
-            }
-            const bool valid = key >= from && key <= pos;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float si = valid ? s[i] * p.scale : -INFINITY;
-                float mx = si;
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-                const float mn = fmaxf(m[i], mx);
-                const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
-                const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
-                float sum = pi;
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, 64);
-                l[i] = l[i] * alpha + sum;
-                m[i] = mn;
-                const uint32_t h = 4 * grp + i;
-                if (h < G) {
-                    sp[wave][col][h] = pi;
-                    if (col == 0) salpha[wave][h] = alpha;
-                }
-            }
+            for (int j = 0; j < 4; j++) kk[nb][j] = *((const u32x4 *)&snew[0][32 * grp] + j);
         }
-        __syncthreads();
-        if (live) {
+        f32x4 s = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s = mfma16(as_bf16x8(qh[j]), as_bf16x8(kk[nb][j]), s);
+            s = mfma16(as_bf16x8(ql[j]), as_bf16x8(kk[nb][j]), s);
+        }
+        const bool valid = key >= from && key <= pos;
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float si = valid ? s[i] * p.scale : -INFINITY;
+            const float mn = fmaxf(m[i], row16_max(si));
+            alpha[i] = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
+            const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
+            l[i] = l[i] * alpha[i] + row16_sum(pi);
+            m[i] = mn;
+            const uint32_t h = 4 * grp + i;
+            if (h < G) sp[wave][col][h] = pi;
+        }
+        // The wave reads back its own LDS writes: in order within a wave, no barrier.
+        __builtin_amdgcn_wave_barrier();
+        // alpha of head h lives in lanes of row-group h/4 (any column): broadcast it.
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float a = __shfl(alpha[h & 3], (h >> 2) * 16, 64);
+            o0[h] *= a;
+            o1[h] *= a;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const uint32_t kpos = kb + i;
+            uint32_t v = (kpos >= from && kpos <= pos) ? vv[nb][i] : 0u;
+            if (STEP && kpos == pos) v = ((const uint32_t *)snew[1])[lane];
+            const float v0 = lo_bf16(v), v1 = hi_bf16(v);
 #pragma unroll
             for (int h = 0; h < G; h++) {
-                const float a = salpha[wave][h];
-                o0[h] *= a;
-                o1[h] *= a;
-            }
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float v0 = lo_bf16(vv[i]), v1 = hi_bf16(vv[i]);
-#pragma unroll
-                for (int h = 0; h < G; h++) {
-                    const float pk = sp[wave][i][h];  // zero for keys outside [from, pos]
-                    o0[h] += pk * v0;
-                    o1[h] += pk * v1;
-                }
+                const float pk = sp[wave][i][h];  // zero for keys outside [from, pos]
+                o0[h] += pk * v0;
+                o1[h] += pk * v1;
             }
         }
-        __syncthreads();
+        __builtin_amdgcn_wave_barrier();
+        TS_MARK(p.marks, 2 + nb);
     }
 
     // Merge the 4 waves of this group.
@@ -244,6 +289,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         so[wave][h][2 * lane + 1] = o1[h];
     }
     __syncthreads();
+    TS_MARK(p.marks, 10);
 
     const uint32_t t = threadIdx.x;
     const size_t gi = (size_t)r * p.kv_heads + kvh;
@@ -265,6 +311,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
             if (d == 0) { mine[h * 130] = M; mine[h * 130 + 1] = L; }
         }
     }
+    TS_MARK(p.marks, 11);
 }
 
 // Merges the partitions of one (row, kv head) in partition order.
@@ -289,20 +336,20 @@ __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t 
 }
 
 struct Split {
-    uint32_t wave_keys, parts, waves;
+    uint32_t wave_keys, parts, waves;  // wave_keys: 16 or 32 (one or two blocks per wave)
 };
 
-Split split(const ts_rows_args *a) {
+Split split(const ts_rows_args *a, bool step) {
     const uint32_t G = a->heads / a->kv_heads;
-    const uint32_t waves = (64 / G) < (uint32_t)kMaxWaves ? 64 / G : kMaxWaves;
+    const uint32_t max_waves = (64 / G) < (uint32_t)kMaxWaves ? 64 / G : kMaxWaves;
     const uint32_t span = a->max_position + 1;
     Split s;
-    s.waves = waves;
-    // Keys per wave (a multiple of 16): as few as cover the span with one group.
-    s.wave_keys = 16;
-    while (s.wave_keys < 64 && s.wave_keys * waves < span) s.wave_keys *= 2;
-    s.parts = (span + waves * s.wave_keys - 1) / (waves * s.wave_keys);
-    if (s.parts == 1) s.waves = (span + s.wave_keys - 1) / s.wave_keys;
+    // One block per wave while a group covers the span, else two.
+    s.wave_keys = span <= max_waves * 16 ? 16 : 32;
+    s.parts = (span + max_waves * s.wave_keys - 1) / (max_waves * s.wave_keys);
+    s.waves = s.parts == 1 ? (span + s.wave_keys - 1) / s.wave_keys : max_waves;
+    // The fused step gives each of its G + 2 rows (q heads, new k, new v) a wave.
+    if (step && s.waves < G + 2) s.waves = (G + 2) < max_waves ? G + 2 : max_waves;
     return s;
 }
 
@@ -328,7 +375,7 @@ int check(const ts_rows_args *a) {
 
 extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
     if (!a || a->kv_heads == 0) return 0;
-    Split s = split(a);
+    Split s = split(a, false);
     if (s.parts <= 1) return 0;
     const size_t G = a->heads / a->kv_heads;
     const size_t groups = (size_t)a->rows * a->kv_heads;
@@ -337,9 +384,14 @@ extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
 
 namespace {
 
+template <int G, bool STEP>
+void (*pick_nb(uint32_t wave_keys))(RowsParams) {
+    return wave_keys == 16 ? attend_rows_kernel<G, STEP, 1> : attend_rows_kernel<G, STEP, 2>;
+}
+
 template <bool STEP>
 int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
-    Split s = split(a);
+    Split s = split(a, STEP);
     p.q = (const float *)a->q; p.k = (const uint16_t *)a->k; p.v = (const uint16_t *)a->v;
     p.out = (float *)a->out; p.slots = a->slots; p.positions = a->positions; p.table = a->kept_table;
     p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads;
@@ -347,6 +399,9 @@ int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
     p.wave_keys = s.wave_keys; p.scale = a->scale;
     p.partials = nullptr;
+#ifdef TS_MARKS
+    p.marks = ts_debug_marks();
+#endif
     if (s.parts > 1) {
         const size_t need = tessera_hip_attend_rows_workspace(a);
         if (!a->workspace || a->workspace_bytes < need)
@@ -356,11 +411,11 @@ int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     void (*k)(RowsParams) = nullptr;
     void (*merge)(RowsParams, uint32_t) = nullptr;
     switch (p.G) {
-    case 1: k = attend_rows_kernel<1, STEP>; merge = attend_rows_merge<1>; break;
-    case 2: k = attend_rows_kernel<2, STEP>; merge = attend_rows_merge<2>; break;
-    case 4: k = attend_rows_kernel<4, STEP>; merge = attend_rows_merge<4>; break;
-    case 8: k = attend_rows_kernel<8, STEP>; merge = attend_rows_merge<8>; break;
-    case 16: k = attend_rows_kernel<16, STEP>; merge = attend_rows_merge<16>; break;
+    case 1: k = pick_nb<1, STEP>(s.wave_keys); merge = attend_rows_merge<1>; break;
+    case 2: k = pick_nb<2, STEP>(s.wave_keys); merge = attend_rows_merge<2>; break;
+    case 4: k = pick_nb<4, STEP>(s.wave_keys); merge = attend_rows_merge<4>; break;
+    case 8: k = pick_nb<8, STEP>(s.wave_keys); merge = attend_rows_merge<8>; break;
+    case 16: k = pick_nb<16, STEP>(s.wave_keys); merge = attend_rows_merge<16>; break;
     default: return ts::fail(TS_ERR_ARG, "attend_rows: %u query heads per kv head (1, 2, 4, 8 or 16)", p.G);
     }
     hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(s.waves * 64), 0, (hipStream_t)stream, p);
@@ -384,8 +439,11 @@ extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
 }
 
 extern "C" int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
-                                       const float *k_gain, float eps, float theta, void *stream) {
-    TS_REQUIRE(a && qkv && q_gain && k_gain, "attend_step: null pointer");
+                                       const float *k_gain, const float *rope_table, uint32_t rope_rows, float eps,
+                                       void *stream) {
+    TS_REQUIRE(a && qkv && q_gain && k_gain && rope_table, "attend_step: null pointer");
+    TS_REQUIRE(a->max_position < rope_rows, "attend_step: positions up to %u but the angle table has %u rows",
+               a->max_position, rope_rows);
     ts_rows_args b = *a;
     b.q = qkv;  // q comes from the product rows; only checked for alignment
     int rc = check(&b);
@@ -393,6 +451,6 @@ extern "C" int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, 
     if (a->rows == 0) return TS_OK;
     RowsParams p;
     memset(&p, 0, sizeof p);
-    p.qkv = qkv; p.q_gain = q_gain; p.k_gain = k_gain; p.eps = eps; p.theta = theta;
+    p.qkv = qkv; p.q_gain = q_gain; p.k_gain = k_gain; p.rope = rope_table; p.eps = eps;
     return launch_rows<true>(&b, p, stream);
 }

@@ -88,15 +88,50 @@ TS_DEV u32x2 e4m3x4_to_bf16x4(uint32_t w) {
 // ---------------------------------------------------------------------------
 // Wave64 reductions (DPP/permute via the compiler's __shfl_xor).
 // ---------------------------------------------------------------------------
+// DPP moves within a row of 16 lanes: quad_perm [1,0,3,2] (xor 1), quad_perm
+// [2,3,0,1] (xor 2), row_half_mirror (lane i <-> 7-i of each 8), row_mirror
+// (i <-> 15-i). After the four steps every lane of the row holds the row's
+// total; each step is one VALU op with a DPP source, not an LDS round trip.
+TS_DEV float dpp_f(float v, int ctrl_id) {
+    const int x = __float_as_int(v);
+    int r;
+    switch (ctrl_id) {
+    case 0: r = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;
+    case 1: r = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break;
+    }
+    return __int_as_float(r);
+}
+
+TS_DEV float row16_sum(float v) {
+    v += dpp_f(v, 0);
+    v += dpp_f(v, 1);
+    v += dpp_f(v, 2);
+    v += dpp_f(v, 3);
+    return v;
+}
+
+TS_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp_f(v, 0));
+    v = fmaxf(v, dpp_f(v, 1));
+    v = fmaxf(v, dpp_f(v, 2));
+    v = fmaxf(v, dpp_f(v, 3));
+    return v;
+}
+
+// Whole-wave totals in every lane: rows by DPP, then two cross-row exchanges.
 TS_DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
 TS_DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    v = row16_max(v);
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    v = fmaxf(v, __shfl_xor(v, 32, 64));
     return v;
 }
 
@@ -108,3 +143,20 @@ TS_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 }
 
 TS_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// In-kernel marks (the reference's TS_MARK ledger, engine/plan/run/src/marks.cuh):
+// with TS_MARKS defined, TS_MARK(ledger, i) records the 100 MHz real-time clock
+// for mark i of this group's first thread into ledger[group * 16 + i].
+#ifdef TS_MARKS
+#define TS_MARK(ledger, i)                                                                      \
+    do {                                                                                        \
+        if ((ledger) && threadIdx.x == 0) {                                                     \
+            const uint32_t _g = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z); \
+            (ledger)[_g * 16 + (i)] = __builtin_amdgcn_s_memrealtime();                         \
+        }                                                                                       \
+    } while (0)
+#else
+#define TS_MARK(ledger, i) \
+    do {                   \
+    } while (0)
+#endif

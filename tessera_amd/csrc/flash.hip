@@ -153,8 +153,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
                 sv[kt] = ok ? s[kt][i] * p.scale : -INFINITY;
                 mx = fmaxf(mx, sv[kt]);
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            mx = row16_max(mx);
             const float mn = fmaxf(m[i], mx);
             const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
             float sum = 0.0f;
@@ -166,8 +165,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
                 sp[wave][0][4 * grp + i][kt * 16 + col] = bf16_bits(ph);
                 sp[wave][1][4 * grp + i][kt * 16 + col] = bf16_bits(pv - ph);
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, 64);
+            sum = row16_sum(sum);
             l[i] = l[i] * alpha + sum;
             m[i] = mn;
 #pragma unroll

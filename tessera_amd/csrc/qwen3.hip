@@ -81,7 +81,7 @@ struct ts_qwen3 {
     float *norm = nullptr;
     std::vector<Layer> layers;
     // activations
-    float *x, *xn, *qkv, *q, *attn, *h, *logits;
+    float *x, *xn, *qkv, *q, *attn, *h, *logits, *rope;
     uint32_t *d_tok, *d_pos, *d_slot, *d_hist, *d_prompt, *d_prompt_pos, *d_prompt_slot, *d_table;
     void *ws = nullptr;
     size_t ws_bytes = 0;
@@ -170,7 +170,7 @@ int run_layers(ts_qwen3 *m, uint32_t rows, const uint32_t *slots, const uint32_t
         if (rows == 1) {
             // q/k norm, RoPE, the kept-row append and attention in one launch (a row
             // may only read keys appended by earlier launches, so one row per slot).
-            TRY(tessera_hip_attend_step(&r, m->qkv, L.q_norm, L.k_norm, c.eps, c.theta, s));
+            TRY(tessera_hip_attend_step(&r, m->qkv, L.q_norm, L.k_norm, m->rope, c.max_context, c.eps, s));
         } else {
             TRY(tessera_hip_qk_norm_rope_append(m->qkv, L.q_norm, L.k_norm, m->q, L.k_cache, L.v_cache, slots,
                                                 pos, m->d_table, rows, c.heads, c.kv_heads, D,
@@ -305,8 +305,9 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
         (rc = m->alloc(&m->d_tok, 1)) || (rc = m->alloc(&m->d_pos, 1)) || (rc = m->alloc(&m->d_slot, 1)) ||
         (rc = m->alloc(&m->d_hist, (size_t)c.max_context + 1)) || (rc = m->alloc(&m->d_prompt, R)) ||
         (rc = m->alloc(&m->d_prompt_pos, R)) || (rc = m->alloc(&m->d_prompt_slot, R)) ||
-        (rc = m->alloc(&m->d_table, m->kept_pages)))
+        (rc = m->alloc(&m->d_table, m->kept_pages)) || (rc = m->alloc(&m->rope, (size_t)c.max_context * D)))
         return fail(rc);
+    if ((rc = tessera_hip_rope_table(m->rope, c.max_context, D, c.theta, m->stream))) return fail(rc);
     m->ws_bytes = workspace_need(m);
     if (m->ws_bytes) {
         char *w = nullptr;

@@ -50,6 +50,17 @@ __global__ __launch_bounds__(256) void rope_kernel(float *x, const uint32_t *pos
     row[b] = va * sn + vb * cs;
 }
 
+// The angle table: (cos, sin) of angle(pos, j, width, theta) for every position
+// and pair, computed once (the reference's `angles` stage, rope.rs:10-58).
+__global__ __launch_bounds__(256) void rope_table_kernel(float2 *t, uint32_t positions, uint32_t width, float theta) {
+    const uint32_t half = width / 2;
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (uint64_t)positions * half) return;
+    float sn, cs;
+    sincosf(rope_angle((uint32_t)(i / half), (uint32_t)(i % half), width, theta), &sn, &cs);
+    t[i] = make_float2(cs, sn);
+}
+
 // ---------------------------------------------------------------------------
 // q/k RmsNorm per head, Halves RoPE, then k and v appended to the kept rows.
 // One wave per (row, head) with width 128: lane j holds the pair (j, j+64),
@@ -238,6 +249,17 @@ extern "C" int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t ro
     hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x,
                        positions, rows, heads, width, theta, (int)halves);
     TS_CHECK_LAUNCH("rope launch");
+    return TS_OK;
+}
+
+extern "C" int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t width, float theta, void *stream) {
+    TS_REQUIRE(table, "rope_table: null pointer");
+    TS_REQUIRE(width >= 2 && width % 2 == 0, "rope_table: width %u must be even", width);
+    const uint64_t n = (uint64_t)positions * (width / 2);
+    if (n == 0) return TS_OK;
+    hipLaunchKernelGGL(rope_table_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (float2 *)table, positions, width, theta);
+    TS_CHECK_LAUNCH("rope_table launch");
     return TS_OK;
 }
 

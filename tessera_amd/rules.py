@@ -126,10 +126,19 @@ def attend_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_page
     return out
 
 
+def rope_table(positions, theta, width=128, device="cuda"):
+    """(cos, sin) of every (position, pair) angle (the "angles" stage)."""
+    t = torch.empty((positions, width // 2, 2), dtype=torch.float32, device=device)
+    abi.call("tessera_hip_rope_table", _ptr(t), positions, width, C.c_float(theta), _stream())
+    return t
+
+
 def attend_step(qkv, q_gain, k_gain, k, v, slots, positions, *, heads, keys, scale, eps, theta, table=None,
-                kept_pages=0, page=16, back=abi.U32_MAX, max_position=None, out=None):
+                kept_pages=0, page=16, back=abi.U32_MAX, max_position=None, out=None, angles=None):
     """Fused decode step: q/k RmsNorm + RoPE from raw product rows, append, attend."""
     rows = qkv.shape[0]
+    if angles is None:
+        angles = rope_table(keys, theta, device=qkv.device)
     if out is None:
         out = torch.empty((rows, heads, 128), dtype=torch.float32, device=qkv.device)
     qshape = torch.empty((rows, heads, 128), device=qkv.device)  # shape carrier only
@@ -137,8 +146,8 @@ def attend_step(qkv, q_gain, k_gain, k, v, slots, positions, *, heads, keys, sca
                   kept_pages=kept_pages, page=page, back=back, max_position=max_position)
     need = abi.load().tessera_hip_attend_rows_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(qkv.device).get(need)
-    abi.call("tessera_hip_attend_step", C.byref(a), _ptr(qkv), _ptr(q_gain), _ptr(k_gain), C.c_float(eps),
-             C.c_float(theta), _stream())
+    abi.call("tessera_hip_attend_step", C.byref(a), _ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(angles),
+             angles.shape[0], C.c_float(eps), _stream())
     return out
 
 

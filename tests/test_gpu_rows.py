@@ -123,3 +123,12 @@ def test_top_k_routing_bit_exact():
     logits[::7, 5] = logits[::7, 9]  # exact ties
     got = from_dev(R().top_k(to_dev(logits, torch), 8))
     assert np.array_equal(got.astype(np.uint32), O.top_k(logits, 8))
+
+
+def test_rope_table_matches_angles():
+    """The angle table against the oracle's angle (cpu.rs:32-34) at Qwen3's theta."""
+    t = from_dev(R().rope_table(200, 1e6)).reshape(200, 64, 2)
+    for pos in (0, 1, 77, 199):
+        for j in (0, 1, 31, 63):
+            ang = O.angle(pos, j, 128, 1e6)
+            assert abs(t[pos, j, 0] - math.cos(ang)) < 2e-6 and abs(t[pos, j, 1] - math.sin(ang)) < 2e-6
