@@ -91,9 +91,9 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
     const uint32_t part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z, parts = gridDim.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
 
-    __shared__ float sp[kWaves][16][G];  // p[key][head] of the current block
+    __shared__ __attribute__((aligned(16))) float sp[kWaves][G][16];  // p[head][key] of the current block
     __shared__ float sm[kWaves][G], sl[kWaves][G];
-    __shared__ float so[kWaves][G][128];
+    __shared__ __attribute__((aligned(16))) float so[kWaves][G][128];
     __shared__ __attribute__((aligned(16))) float sq[STEP ? G : 1][128];          // fused step: q heads
     __shared__ __attribute__((aligned(16))) uint16_t snew[STEP ? 2 : 1][128];     // fused step: new k, v
 
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         kgb = p.k_gain[lane + 64];
     }
     u32x4 kk[NB][4];
-    uint32_t vv[NB][16];
+    u32x4 vq[NB][4];  // V: load j holds key 4j + lane/16 of the block, dims 8*(lane%16)..+8
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
         // 16 rows of one page (pages hold >= 16 rows); dense rows clamp at the
@@ -149,8 +149,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
 #pragma unroll
         for (int j = 0; j < 4; j++) kk[nb][j] = *((const u32x4 *)kr + j);
 #pragma unroll
-        for (int i = 0; i < 16; i++)
-            vv[nb][i] = *((const uint32_t *)(p.v + ((row0 + min((uint32_t)i, room)) * p.kv_heads + kvh) * 128) + lane);
+        for (int j = 0; j < 4; j++) {
+            const uint32_t i = 4 * j + grp;
+            vq[nb][j] = *(const u32x4 *)(p.v + ((row0 + min(i, room)) * p.kv_heads + kvh) * 128 + 8 * col);
+        }
     }
 
     if (STEP) {
@@ -180,30 +182,28 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         }
         __syncthreads();
         TS_MARK(p.marks, 1);
-        if (part == 0) {
-            // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198).
-            const uint64_t row = kept_row(p, slot, pos);
-            for (uint32_t i = threadIdx.x; i < 128; i += blockDim.x) {
-                const uint32_t which = i >> 6;
-                uint16_t *dst = (uint16_t *)(which == 0 ? p.k : p.v) + (row * p.kv_heads + kvh) * 128;
-                ((uint32_t *)dst)[i & 63] = ((const uint32_t *)snew[which])[i & 63];
-            }
-        }
     }
 
     // q operand: row (head) col of the group, d-group grp; two bf16 parts.
+    // Read as 16-byte vectors from a row that exists, then zeroed past G.
     u32x4 qh[4], ql[4];
     {
         const bool ok = col < G;
-        const float *qr = STEP ? &sq[ok ? col : 0][32 * grp]
-                               : p.q + ((size_t)r * p.heads + kvh * G + (ok ? col : 0)) * 128 + 32 * grp;
+        const uint32_t qrow = ok ? col : 0;
+        const float4 *qr = STEP ? (const float4 *)&sq[qrow][32 * grp]
+                                : (const float4 *)(p.q + ((size_t)r * p.heads + kvh * G + qrow) * 128 + 32 * grp);
+        float4 qv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) qv[i] = qr[i];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
+            const float f[8] = {qv[2 * j].x, qv[2 * j].y, qv[2 * j].z, qv[2 * j].w,
+                                qv[2 * j + 1].x, qv[2 * j + 1].y, qv[2 * j + 1].z, qv[2 * j + 1].w};
             uint32_t h[4], l[4];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                float a = ok ? qr[8 * j + 2 * e] : 0.0f, b = ok ? qr[8 * j + 2 * e + 1] : 0.0f;
-                float ha = bf16_round(a), hb = bf16_round(b);
+                const float a = ok ? f[2 * e] : 0.0f, b = ok ? f[2 * e + 1] : 0.0f;
+                const float ha = bf16_round(a), hb = bf16_round(b);
                 h[e] = pack_bf16x2(ha, hb);
                 l[e] = pack_bf16x2(a - ha, b - hb);
             }
@@ -212,14 +212,21 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         }
     }
 
+#ifdef TS_MARKS
+    __builtin_amdgcn_s_waitcnt(0xc070);  // debug marks only: wait for every load, then stamp
+    TS_MARK(p.marks, 8);
+#endif
     // Online softmax state: this lane's 4 head rows (4*grp + i) in the S layout.
     float m[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
-    // Accumulator: heads h < G, dims 2*lane, 2*lane+1.
-    float o0[G], o1[G];
+    // Accumulator: heads h < G; lane holds dims 8*(lane%16)..+8 summed over the
+    // keys with index = lane/16 (mod 4); the four lane groups add up at the end.
+    float o[G][8];
 #pragma unroll
-    for (int h = 0; h < G; h++) { o0[h] = 0.0f; o1[h] = 0.0f; }
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
 
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
@@ -247,7 +254,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
             l[i] = l[i] * alpha[i] + row16_sum(pi);
             m[i] = mn;
             const uint32_t h = 4 * grp + i;
-            if (h < G) sp[wave][col][h] = pi;
+            if (h < G) sp[wave][h][col] = pi;
         }
         // The wave reads back its own LDS writes: in order within a wave, no barrier.
         __builtin_amdgcn_wave_barrier();
@@ -255,27 +262,31 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
 #pragma unroll
         for (int h = 0; h < G; h++) {
             const float a = __shfl(alpha[h & 3], (h >> 2) * 16, 64);
-            o0[h] *= a;
-            o1[h] *= a;
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[h][e] *= a;
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const uint32_t kpos = kb + i;
-            uint32_t v = (kpos >= from && kpos <= pos) ? vv[nb][i] : 0u;
-            if (STEP && kpos == pos) v = ((const uint32_t *)snew[1])[lane];
-            const float v0 = lo_bf16(v), v1 = hi_bf16(v);
+        for (int j = 0; j < 4; j++) {
+            const uint32_t i = 4 * j + grp, kpos = kb + i;
+            u32x4 v = vq[nb][j];
+            if (STEP && kpos == pos) v = *(const u32x4 *)&snew[1][8 * col];
+            const bool ok = kpos >= from && kpos <= pos;  // p is zero outside; keep v finite too
+            const uint32_t w4[4] = {ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 #pragma unroll
             for (int h = 0; h < G; h++) {
-                const float pk = sp[wave][i][h];  // zero for keys outside [from, pos]
-                o0[h] += pk * v0;
-                o1[h] += pk * v1;
+                const float pk = sp[wave][h][i];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    o[h][2 * e] += pk * lo_bf16(w4[e]);
+                    o[h][2 * e + 1] += pk * hi_bf16(w4[e]);
+                }
             }
         }
         __builtin_amdgcn_wave_barrier();
         TS_MARK(p.marks, 2 + nb);
     }
 
-    // Merge the 4 waves of this group.
+    // Merge the waves of this group.
     if (col == 0) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -284,9 +295,20 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         }
     }
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        so[wave][h][2 * lane] = o0[h];
-        so[wave][h][2 * lane + 1] = o1[h];
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = o[h][e];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            o[h][e] = v;
+        }
+    if (grp == 0) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            *(float4 *)&so[wave][h][8 * col] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            *(float4 *)&so[wave][h][8 * col + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+        }
     }
     __syncthreads();
     TS_MARK(p.marks, 10);
@@ -309,6 +331,17 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         } else {
             mine[h * 130 + 2 + d] = O;
             if (d == 0) { mine[h * 130] = M; mine[h * 130 + 1] = L; }
+        }
+    }
+    if (STEP && part == 0) {
+        // The new row joins the kept rows (Store::append, engine/ir/interp/src/
+        // run.rs:122-198). Stored last: a store the compiler cannot prove apart from
+        // the K/V loads would otherwise wait for all of them.
+        const uint64_t row = kept_row(p, slot, pos);
+        for (uint32_t i = threadIdx.x; i < 128; i += blockDim.x) {
+            const uint32_t which = i >> 6;
+            uint16_t *dst = (uint16_t *)(which == 0 ? p.k : p.v) + (row * p.kv_heads + kvh) * 128;
+            ((uint32_t *)dst)[i & 63] = ((const uint32_t *)snew[which])[i & 63];
         }
     }
     TS_MARK(p.marks, 11);
