@@ -68,8 +68,15 @@ def lm_head_roofline(torch, reps=20):
     torch.cuda.synchronize()
     t = s.elapsed_time(e) / 1e3 / reps
     nbytes = n * k * 2 + k * 4 * 2 + n * 4  # weights, x and gain, logits
+    # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    # (profiles/lanes_lm_head_traffic.txt), scaled by a plain copy of known size.
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "lanes_lm_head_traffic.json")
+    if os.path.exists(prof):
+        traffic = json.load(open(prof))["traffic_bytes_per_launch"]
     return {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": nbytes / t / HBM_PEAK, "traffic": None, "kernel": "lanes_kernel (lm_head 151936x1024)",
+            "frac": nbytes / t / HBM_PEAK, "traffic": traffic,
+            "kernel": "ts::gemv_kernel<1,8,f32 x,bf16 w> (lanes, lm_head 151936x1024, fused RmsNorm)",
             "bytes_per_launch": nbytes, "us_per_launch": t * 1e6}
 
 
