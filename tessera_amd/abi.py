@@ -108,18 +108,21 @@ def load():
     return lib
 
 
-def declared_functions() -> list[str]:
-    """Every function the public header declares (checked against the exports)."""
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(tessera_hip_\w+)\s*\(", text)))
+def _header_text(header=None) -> str:
+    paths = [header] if header else sorted(
+        os.path.join(os.path.dirname(HEADER), f) for f in os.listdir(os.path.dirname(HEADER)) if f.endswith(".h"))
+    return re.sub(r"/\*.*?\*/", "", "".join(open(p).read() for p in paths), flags=re.S)
 
 
-def declared_arity() -> dict[str, int]:
-    """Parameter count of each prototype in the public header."""
-    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+def declared_functions(header=None) -> list[str]:
+    """Every function the public headers declare (checked against the exports)."""
+    return sorted(set(re.findall(r"\b(tessera_\w+)\s*\(", _header_text(header))))
+
+
+def declared_arity(header=None) -> dict[str, int]:
+    """Parameter count of each prototype in the public headers."""
     out = {}
-    for name, params in re.findall(r"\b(tessera_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+    for name, params in re.findall(r"\b(tessera_\w+)\s*\(([^)]*)\)\s*;", _header_text(header)):
         params = params.strip()
         out[name] = 0 if params in ("", "void") else params.count(",") + 1
     return out
