@@ -231,6 +231,8 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL)) == 0, "tiled: unknown stage bits %#x",
                a->stages);
     TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "tiled: x and w must be 16-byte aligned");
+    const int big = ts::tiled_big_launch(a, stream);
+    if (big != 1) return big;
     const bool silu = a->stages & TS_AFTER_SILU_MUL;
     TiledParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;

@@ -62,6 +62,23 @@ def test_linear_bf16_sweep_shapes(m, k, n):
     assert max_rel(got16, want) <= 2e-2
 
 
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 256), (2000, 7777, 192), (2000, 7777, 136)])
+def test_tiled_256_tiles(m, n, k):
+    """Products with enough 256x256 tiles take the big-tile kernel (bf16 x and w)."""
+    R = _rules()
+    O.set_threads(O.lib().or_threads_available())
+    r = rng(m + n + k)
+    xb, xf = bf16_bits_normal(r, (m, k))
+    wb, wf = bf16_bits_normal(r, (n, k))
+    want = O.product_bf16w(xf, wb)
+    O.set_threads(1)
+    res = r.standard_normal((m, n)).astype(np.float32)
+    got = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), a0=to_dev(res, torch)))
+    _check(got, want + res, _bound(xf, wf) + 1e-5)
+    got16 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), out_dtype=torch.bfloat16))
+    assert max_rel(got16, want) <= 2e-2
+
+
 def test_lanes_and_tiled_agree_at_16_rows():
     R = _rules()
     r = rng(5)
