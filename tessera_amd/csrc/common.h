@@ -146,6 +146,10 @@ TS_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// D = A * B^T + C on a 32 x 32 x 16 tile. A lane l: row l % 32, k 8 (l / 32) .. +7;
+// B likewise by column; D lane l: column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
+TS_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+
 TS_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // In-kernel marks (the reference's TS_MARK ledger, engine/plan/run/src/marks.cuh):

@@ -13,8 +13,8 @@
 //    B 256 x 64 bf16, 128-byte rows with 16-byte chunks XOR-swizzled by row). The
 //    stages fill with global_load_lds_dwordx4, straight from HBM to LDS (no staging
 //    registers), and the next stage's loads overlap the current stage's MFMAs.
-//  * Both 32-deep substeps' fragments are read from LDS before the 64 MFMAs that
-//    use them, so LDS latency hides under matrix work.
+//  * Scheduling groups pin the order: one substep's fragment reads, then its MFMAs
+//    interleaved with the other substep's reads and the next stage's loads.
 //  * 128 KiB of dynamic LDS per group (gfx950 has 160 KiB per CU): one group per CU.
 #include "common.h"
 
@@ -59,6 +59,55 @@ TS_DEV void fetch_stage(const BigParams &p, char *stage, uint32_t m0, uint32_t n
     }
 }
 
+// s_waitcnt immediate for vmcnt(0) expcnt(7) lgkmcnt(0) (gfx9 packs vmcnt's high
+// bits at 15:14; they stay zero).
+constexpr int kWaitAll = 0x0070;
+
+// One 64-deep step over stage s & 1: 2 x 12 fragment reads, 64 MFMAs and, when
+// FETCH, the 8 loads that fill the other stage for step s + 1. The order is pinned
+// with scheduling groups: the first substep's reads, then its MFMAs interleaved
+// with the second substep's reads and the next stage's loads, then the second
+// substep's MFMAs, so LDS and HBM latency hide under matrix work.
+template <bool FETCH>
+TS_DEV void mfma_step(const BigParams &p, char *lds, uint32_t s, f32x4 (&acc)[8][4], uint32_t m0, uint32_t n0,
+                      uint32_t wave, uint32_t lane, uint32_t wm, uint32_t wn, uint32_t col, uint32_t grp) {
+    const char *sa = lds + (s & 1) * 2 * kStage, *sb = sa + kStage;
+    bf16x8 af[2][8], bfr[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const uint32_t c = ks * 4 + grp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) bfr[ks][j] = as_bf16x8(*(const u32x4 *)(sb + swz(wn * 64 + j * 16 + col, c)));
+#pragma unroll
+        for (int i = 0; i < 8; i++) af[ks][i] = as_bf16x8(*(const u32x4 *)(sa + swz(wm * 128 + i * 16 + col, c)));
+    }
+    if (FETCH) fetch_stage(p, lds + ((s + 1) & 1) * 2 * kStage, m0, n0, (s + 1) * BK, wave, lane);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma16(af[ks][i], bfr[ks][j], acc[i][j]);
+    // Masks: 0x008 MFMA, 0x020 VMEM read, 0x100 DS read.
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
+#pragma unroll
+    for (int i = 0; i < 12; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    if (FETCH) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 44, 0);
+    } else {
+        __builtin_amdgcn_sched_group_barrier(0x008, 52, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // nothing moves past here (the wait and barrier follow)
+}
+
 __global__ __launch_bounds__(kThreads, 1) void tiled_big_kernel(BigParams p) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const uint32_t t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -81,31 +130,15 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_big_kernel(BigParams p) {
 
     const uint32_t steps = p.k / BK;
     fetch_stage(p, lds, m0, n0, 0, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0xc070);  // vmcnt(0): this wave's stage loads are in LDS
+    __builtin_amdgcn_s_waitcnt(kWaitAll);  // this wave's stage loads are in LDS
     __syncthreads();
-    for (uint32_t s = 0; s < steps; s++) {
-        char *cur = lds + (s & 1) * 2 * kStage;
+    for (uint32_t s = 0; s + 1 < steps; s++) {
         // The other stage was last read before the previous barrier: refill it now.
-        if (s + 1 < steps) fetch_stage(p, lds + ((s + 1) & 1) * 2 * kStage, m0, n0, (s + 1) * BK, wave, lane);
-        const char *sa = cur, *sb = cur + kStage;
-        bf16x8 af[2][8], bfr[2][4];
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-            const uint32_t c = ks * 4 + grp;
-#pragma unroll
-            for (int j = 0; j < 4; j++) bfr[ks][j] = as_bf16x8(*(const u32x4 *)(sb + swz(wn * 64 + j * 16 + col, c)));
-#pragma unroll
-            for (int i = 0; i < 8; i++) af[ks][i] = as_bf16x8(*(const u32x4 *)(sa + swz(wm * 128 + i * 16 + col, c)));
-        }
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++)
-#pragma unroll
-            for (int i = 0; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = mfma16(af[ks][i], bfr[ks][j], acc[i][j]);
-        __builtin_amdgcn_s_waitcnt(0xc070);  // the next stage's loads have landed
+        mfma_step<true>(p, lds, s, acc, m0, n0, wave, lane, wm, wn, col, grp);
+        __builtin_amdgcn_s_waitcnt(kWaitAll);  // the next stage's loads have landed
         __syncthreads();
     }
+    mfma_step<false>(p, lds, steps - 1, acc, m0, n0, wave, lane, wm, wn, col, grp);
 
     // Epilogue. D lane layout: column col, rows 4*grp + r of each 16x16 tile.
     const uint32_t N = p.n, M = p.m;

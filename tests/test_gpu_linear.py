@@ -62,9 +62,11 @@ def test_linear_bf16_sweep_shapes(m, k, n):
     assert max_rel(got16, want) <= 2e-2
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 8192, 256), (2000, 7777, 192), (2000, 7777, 136)])
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 256), (2000, 7777, 192), (2000, 7777, 136), (1300, 12300, 64),
+                                   (4096, 16384, 128)])
 def test_tiled_256_tiles(m, n, k):
-    """Products with enough 256x256 tiles take the big-tile kernel (bf16 x and w)."""
+    """Products with enough 256x256 tiles take the big-tile kernel (bf16 x and w): one
+    tile per CU, ragged edges, several tiles per CU (4096 x 16384)."""
     R = _rules()
     O.set_threads(O.lib().or_threads_available())
     r = rng(m + n + k)
