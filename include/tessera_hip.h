@@ -96,6 +96,40 @@ size_t tessera_hip_lanes_workspace(const ts_linear_args *a);
 int tessera_hip_tiled(const ts_linear_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------
+ * Picked: row r multiplies matrix ids[r] - first of a stored set (the MoE expert
+ * products). out[r, c] = sum_k x[r / repeat, k] * w[ids[r] - first][offset + c, k];
+ * rows whose id is outside [first, first + count) read zeros.
+ * w: [count, stride, k] bf16, or e4m3 with a bf16 scale per stored row
+ * (w_scale [count, stride]). With TS_AFTER_SILU_MUL the matrix rows offset..
+ * offset+n are the gates and offset+n..offset+2n the ups: out = silu(g) * u.
+ * x: [rows / repeat, k] f32 or bf16; out: [rows, n] f32 or bf16.
+ * Rows are sorted by matrix (a stable counting sort, in the workspace), then each
+ * matrix's rows run as dense MFMA row tiles against one read of its weights.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void *x;        /* [rows / repeat, k] */
+    const void *w;        /* [count, stride, k] */
+    const void *w_scale;  /* [count, stride] bf16, e4m3 weights only */
+    const uint32_t *ids;  /* [rows] */
+    void *out;            /* [rows, n] */
+    void *workspace;
+    size_t workspace_bytes;
+    uint32_t rows, n, k;
+    uint32_t count;       /* matrices of the set held here */
+    uint32_t stride;      /* rows per stored matrix */
+    uint32_t offset;      /* first matrix row used */
+    uint32_t repeat;      /* consecutive rows sharing one x row (the picks per token) */
+    uint32_t first;       /* id of this set's first matrix */
+    int32_t x_dtype, w_dtype, out_dtype;
+    uint32_t stages;      /* 0 or TS_AFTER_SILU_MUL */
+} ts_picked_args;
+
+/* Replaces: rule "picked" (engine/rules/linear/src/picked.rs:28-60,106-122) on the
+ * site Picked (engine/plan/lower/src/sites/matmul.rs:10-24,66-96). */
+int tessera_hip_picked(const ts_picked_args *a, void *stream);
+size_t tessera_hip_picked_workspace(const ts_picked_args *a);
+
+/* ----------------------------------------------------------------------------
  * Ragged-row attention over kept (paged) K/V.
  * Row r (slot s, position p) attends keys [max(0, p - back), p] of slot s; the
  * key at position j lives at kept row table[s*kept_pages + (j >> log2 page)]
@@ -196,6 +230,23 @@ int tessera_hip_qk_norm_rope_append(const float *qkv, const float *q_gain, const
  * Replaces: "gather" (engine/rules/kernels/src/gather.rs; interp cpu.rs:511-525). */
 int tessera_hip_gather(const void *table, const uint32_t *ids, float *out, uint32_t count,
                        uint32_t table_rows, uint32_t width, uint32_t first, void *stream);
+
+/* out[j] = x[j / picks, ids[j]], zero when ids[j] >= width; x [rows, width],
+ * ids/out [rows, picks]. Replaces: interp take (engine/ir/interp/src/cpu.rs:498-508)
+ * as the MoE layer uses it (engine/models/src/decoder.rs:78). */
+int tessera_hip_take(const float *x, const uint32_t *ids, float *out, uint32_t rows, uint32_t width,
+                     uint32_t picks, void *stream);
+
+/* Row softmax in the reference's order: max from -inf (NaN ignored), exp(v - max),
+ * sequential sum, divide. One thread per row: routing widths (<= 4096).
+ * Replaces: interp softmax (engine/ir/interp/src/cpu.rs:49-59). out may alias x. */
+int tessera_hip_softmax(const float *x, float *out, uint32_t rows, uint32_t width, void *stream);
+
+/* out[o, i] = sum_t x[o, t, i] * weights[o, t] (t in order from 0, no fused
+ * multiply-add: bit-exact), or the mean when weights is NULL. x [outer, count, inner].
+ * Replaces: mean / mix (engine/ir/interp/src/cpu.rs:450-473), the MoE combine. */
+int tessera_hip_mix(const float *x, const float *weights, float *out, uint32_t outer, uint32_t count,
+                    uint32_t inner, void *stream);
 
 /* ids[r] = first index of the largest finite entry of row r (NaN and -inf
  * skipped; `width` when none). x f32 [rows, width].

@@ -54,10 +54,22 @@ class RowsArgs(C.Structure):
     ]
 
 
+class PickedArgs(C.Structure):
+    """ts_picked_args (include/tessera_hip.h)."""
+    _fields_ = [
+        ("x", C.c_void_p), ("w", C.c_void_p), ("w_scale", C.c_void_p), ("ids", C.c_void_p),
+        ("out", C.c_void_p), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t),
+        ("rows", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("count", C.c_uint32),
+        ("stride", C.c_uint32), ("offset", C.c_uint32), ("repeat", C.c_uint32), ("first", C.c_uint32),
+        ("x_dtype", C.c_int32), ("w_dtype", C.c_int32), ("out_dtype", C.c_int32), ("stages", C.c_uint32),
+    ]
+
+
 _P = C.c_void_p
 _U = C.c_uint32
 _LA = C.POINTER(LinearArgs)
 _RA = C.POINTER(RowsArgs)
+_PA = C.POINTER(PickedArgs)
 
 SIGNATURES = {
     "tessera_hip_init": (C.c_int, []),
@@ -68,6 +80,11 @@ SIGNATURES = {
     "tessera_hip_lanes": (C.c_int, [_LA, _P]),
     "tessera_hip_lanes_workspace": (C.c_size_t, [_LA]),
     "tessera_hip_tiled": (C.c_int, [_LA, _P]),
+    "tessera_hip_picked": (C.c_int, [_PA, _P]),
+    "tessera_hip_picked_workspace": (C.c_size_t, [_PA]),
+    "tessera_hip_take": (C.c_int, [_P, _P, _P, _U, _U, _U, _P]),
+    "tessera_hip_softmax": (C.c_int, [_P, _P, _U, _U, _P]),
+    "tessera_hip_mix": (C.c_int, [_P, _P, _P, _U, _U, _U, _P]),
     "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
     "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),

@@ -44,6 +44,17 @@ int gemv_launch(const ts_linear_args *a, void *stream);
 // product is not its shape (bf16 x and w, no SiLU pair, enough tiles), else an error.
 int tiled_big_launch(const ts_linear_args *a, void *stream);
 
+// Rows of a picked product sorted by matrix (moe.hip), in the caller's workspace.
+struct Route {
+    uint32_t *row_start;   // [count + 2]: first sorted position per bucket (the last: out-of-range ids)
+    uint32_t *tile_start;  // [count + 1]: first row tile per matrix
+    uint32_t *perm;        // [rows]: row at each sorted position
+};
+size_t route_words(uint32_t rows, uint32_t count);
+int route_launch(const uint32_t *ids, uint32_t rows, uint32_t first, uint32_t count, uint32_t tile_rows, void *ws,
+                 Route *route, void *stream);
+int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n, int out_bf16, void *stream);
+
 }  // namespace ts
 
 // ---------------------------------------------------------------------------

@@ -37,6 +37,12 @@ struct TiledParams {
     uint32_t m, n, k;
     uint32_t stages;
     int out_bf16;
+    // Picked products (PICK): rows sorted by matrix. perm[pos] is the row at sorted
+    // position pos; matrix e owns positions [row_start[e], row_start[e + 1]) and
+    // row tiles [tile_start[e], tile_start[e + 1]). Row r reads x row r / repeat;
+    // matrix e's rows start at w + (e * stride + offset) * k (scales likewise).
+    const uint32_t *perm, *row_start, *tile_start;
+    uint32_t matrices, repeat, stride, offset;
 };
 
 // Byte offset of (row, chunk) in a swizzled [128 rows][8 chunks of 16B] tile.
@@ -46,6 +52,11 @@ template <bool XF32, bool W8, bool SILU>
 struct Loader {
     // Per thread per stage: A: 4 chunks (rows t/8 + 32i, chunk t%8), B: 4 chunks.
     u32x4 a_hi[4], a_lo[4], b[4];
+    // x row of each of this thread's 4 A rows, or -1 for a zero row.
+    int64_t src[4];
+    // The weights of this tile's matrix (the whole w outside picked products).
+    const void *w;
+    const uint16_t *w_scale;
 
     // Weight row of B-tile row `br` for this output tile.
     TS_DEV static uint32_t wrow(uint32_t br, uint32_t n0, uint32_t N) {
@@ -61,12 +72,12 @@ struct Loader {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t r = (t >> 3) + 32 * i;
-            const uint32_t m = m0 + r;
+            const bool ain = src[i] >= 0 && kin;
             if (XF32) {
                 float v[8];
-                if (m < p.m && kin) {
-                    const float4 *src = (const float4 *)((const float *)p.x + (size_t)m * p.k + kk);
-                    float4 u0 = src[0], u1 = src[1];
+                if (ain) {
+                    const float4 *src4 = (const float4 *)((const float *)p.x + (size_t)src[i] * p.k + kk);
+                    float4 u0 = src4[0], u1 = src4[1];
                     v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
                     v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
                 } else {
@@ -84,22 +95,21 @@ struct Loader {
                 a_hi[i] = u32x4{h[0], h[1], h[2], h[3]};
                 a_lo[i] = u32x4{l[0], l[1], l[2], l[3]};
             } else {
-                a_hi[i] = (m < p.m && kin) ? *(const u32x4 *)((const uint16_t *)p.x + (size_t)m * p.k + kk)
-                                           : u32x4{0, 0, 0, 0};
+                a_hi[i] = ain ? *(const u32x4 *)((const uint16_t *)p.x + (size_t)src[i] * p.k + kk) : u32x4{0, 0, 0, 0};
             }
             const uint32_t nr = wrow(r, n0, p.n);
             const uint32_t nrows = SILU ? 2 * p.n : p.n;
             const bool nin = (SILU ? (n0 + (r >> 6) * 32 + (r & 31)) < p.n : nr < nrows) && kin;
             if (W8) {
                 if (nin) {
-                    const u32x2 c = *(const u32x2 *)((const uint8_t *)p.w + (size_t)nr * p.k + kk);
+                    const u32x2 c = *(const u32x2 *)((const uint8_t *)w + (size_t)nr * p.k + kk);
                     u32x2 lo = e4m3x4_to_bf16x4(c.x), hi = e4m3x4_to_bf16x4(c.y);
                     b[i] = u32x4{lo.x, lo.y, hi.x, hi.y};
                 } else {
                     b[i] = u32x4{0, 0, 0, 0};
                 }
             } else {
-                b[i] = nin ? *(const u32x4 *)((const uint16_t *)p.w + (size_t)nr * p.k + kk) : u32x4{0, 0, 0, 0};
+                b[i] = nin ? *(const u32x4 *)((const uint16_t *)w + (size_t)nr * p.k + kk) : u32x4{0, 0, 0, 0};
             }
         }
     }
@@ -116,16 +126,47 @@ struct Loader {
     }
 };
 
-template <bool XF32, bool W8, bool SILU>
+template <bool XF32, bool W8, bool SILU, bool PICK>
 __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
     constexpr int TILE = BM * BK * 2;  // bytes of one operand stage
     __shared__ __attribute__((aligned(16))) char lds[2][XF32 ? 3 : 2][TILE];
+    __shared__ uint32_t rows_out[PICK ? BM : 1];  // output row of each tile row (PICK)
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
     const uint32_t col = lane & 15, grp = lane >> 4;
-    const uint32_t m0 = blockIdx.y * BM;
     const uint32_t n0 = blockIdx.x * (SILU ? BN / 2 : BN);  // SILU: 64 output columns per tile
+
+    Loader<XF32, W8, SILU> ld;
+    uint32_t m0 = blockIdx.y * BM, mend = p.m;  // tile rows [m0, min(m0 + BM, mend))
+    ld.w = p.w;
+    ld.w_scale = p.w_scale;
+    if (PICK) {
+        // Row tile blockIdx.y belongs to the matrix e with tile_start[e] <= y < tile_start[e + 1].
+        const uint32_t y = blockIdx.y;
+        if (y >= p.tile_start[p.matrices]) return;
+        uint32_t lo = 0, hi = p.matrices;  // invariant: tile_start[lo] <= y < tile_start[hi]
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) / 2;
+            if (p.tile_start[mid] <= y) lo = mid;
+            else hi = mid;
+        }
+        const uint32_t e = lo;
+        m0 = p.row_start[e] + (y - p.tile_start[e]) * BM;
+        mend = p.row_start[e + 1];
+        const size_t first_row = (size_t)e * p.stride + p.offset;
+        ld.w = (const char *)p.w + first_row * p.k * (W8 ? 1 : 2);
+        if (W8) ld.w_scale = p.w_scale + first_row;
+        for (uint32_t r = threadIdx.x; r < BM; r += kThreads)
+            rows_out[r] = m0 + r < mend ? p.perm[m0 + r] : 0xffffffffu;
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = (threadIdx.x >> 3) + 32 * i;
+        if (PICK) ld.src[i] = rows_out[r] != 0xffffffffu ? (int64_t)(rows_out[r] / p.repeat) : -1;
+        else ld.src[i] = m0 + r < p.m ? (int64_t)(m0 + r) : -1;
+    }
 
     f32x4 acc[4][4];
 #pragma unroll
@@ -133,7 +174,6 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0, 0, 0, 0};
 
-    Loader<XF32, W8, SILU> ld;
     const uint32_t steps = (p.k + BK - 1) / BK;
     ld.fetch(p, m0, n0, 0);
     ld.store(lds[0][0], lds[0][XF32 ? 2 : 0], lds[0][1]);
@@ -171,20 +211,22 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
     }
 
     // Epilogue. D lane layout: column col, rows 4*grp + r of each 16x16 tile.
-    const uint32_t N = p.n, M = p.m;
+    const uint32_t N = p.n;
+    const uint16_t *scale = ld.w_scale;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t m = m0 + wm * 64 + i * 16 + 4 * grp + r;
-            if (m >= M) continue;
+            const uint32_t tr = wm * 64 + i * 16 + 4 * grp + r;
+            if (m0 + tr >= mend) continue;
+            const uint32_t m = PICK ? rows_out[tr] : m0 + tr;
             if (!SILU) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const uint32_t n = n0 + wn * 64 + j * 16 + col;
                     if (n >= N) continue;
                     float v = acc[i][j][r];
-                    if (W8) v *= bf16_float(p.w_scale[n]);
+                    if (W8) v *= bf16_float(scale[n]);
                     if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
                     if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
                     else ((float *)p.out)[(size_t)m * N + n] = v;
@@ -196,8 +238,8 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
                     if (n >= N) continue;
                     float g = acc[i][j][r], u = acc[i][j + 2][r];
                     if (W8) {
-                        g *= bf16_float(p.w_scale[n]);
-                        u *= bf16_float(p.w_scale[N + n]);
+                        g *= bf16_float(scale[n]);
+                        u *= bf16_float(scale[N + n]);
                     }
                     float v = g / (1.0f + expf(-g)) * u;
                     if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
@@ -211,9 +253,15 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
 
 using Kern = void (*)(TiledParams);
 
-template <bool XF32, bool W8>
-Kern pick(bool silu) {
-    return silu ? tiled_kernel<XF32, W8, true> : tiled_kernel<XF32, W8, false>;
+template <bool XF32, bool W8, bool PICK>
+Kern pick_silu(bool silu) {
+    return silu ? tiled_kernel<XF32, W8, true, PICK> : tiled_kernel<XF32, W8, false, PICK>;
+}
+
+template <bool PICK>
+Kern pick_kernel(bool xf, bool w8, bool silu) {
+    return xf ? (w8 ? pick_silu<true, true, PICK>(silu) : pick_silu<true, false, PICK>(silu))
+              : (w8 ? pick_silu<false, true, PICK>(silu) : pick_silu<false, false, PICK>(silu));
 }
 
 }  // namespace
@@ -240,11 +288,64 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     const uint32_t cols = silu ? BN / 2 : BN;
     const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->m + BM - 1) / BM;
     TS_REQUIRE(gy <= 65535, "tiled: m=%u too large for one launch", a->m);
-    const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
-    Kern k = xf ? (w8 ? pick<true, true>(silu) : pick<true, false>(silu))
-                : (w8 ? pick<false, true>(silu) : pick<false, false>(silu));
+    p.perm = p.row_start = p.tile_start = nullptr;
+    p.matrices = 0; p.repeat = 1; p.stride = 0; p.offset = 0;
+    Kern k = pick_kernel<false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("tiled launch");
+    return TS_OK;
+}
+
+static int picked_check(const ts_picked_args *a) {
+    TS_REQUIRE(a && a->x && a->w && a->ids && a->out, "picked: null pointer");
+    TS_REQUIRE(a->n >= 1 && a->k >= 1, "picked: empty product n=%u k=%u", a->n, a->k);
+    TS_REQUIRE(a->k % 8 == 0, "picked: k=%u must be a multiple of 8", a->k);
+    TS_REQUIRE(a->count >= 1 && a->count <= 16384, "picked: count=%u (1..16384 matrices)", a->count);
+    TS_REQUIRE(a->repeat >= 1, "picked: repeat 0");
+    const uint32_t used = (a->stages & TS_AFTER_SILU_MUL) ? 2 * a->n : a->n;
+    TS_REQUIRE((uint64_t)a->offset + used <= a->stride, "picked: rows %u..%u outside a matrix of %u rows", a->offset,
+               a->offset + used, a->stride);
+    TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "picked: x dtype %d", a->x_dtype);
+    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3, "picked: w dtype %d", a->w_dtype);
+    TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "picked: out dtype %d", a->out_dtype);
+    TS_REQUIRE(a->w_dtype != TS_E4M3 || a->w_scale, "picked: e4m3 weights need w_scale");
+    TS_REQUIRE((a->stages & ~TS_AFTER_SILU_MUL) == 0, "picked: stage bits %#x (only TS_AFTER_SILU_MUL)", a->stages);
+    TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "picked: x and w must be 16-byte aligned");
+    TS_REQUIRE((uint64_t)a->rows / BM + a->count <= 65535, "picked: %u rows and %u matrices in one launch", a->rows,
+               a->count);
+    return TS_OK;
+}
+
+extern "C" size_t tessera_hip_picked_workspace(const ts_picked_args *a) {
+    if (!a) return 0;
+    return ts::route_words(a->rows, a->count) * sizeof(uint32_t);
+}
+
+extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
+    const int bad = picked_check(a);
+    if (bad) return bad;
+    if (a->rows == 0) return TS_OK;
+    const size_t need = tessera_hip_picked_workspace(a);
+    if (!a->workspace || a->workspace_bytes < need)
+        return ts::fail(TS_ERR_WORKSPACE, "picked: workspace %zu bytes, need %zu", a->workspace_bytes, need);
+    TS_REQUIRE(ts::aligned(a->workspace, 4), "picked: workspace must be 4-byte aligned");
+    ts::Route route;
+    int rc = ts::route_launch(a->ids, a->rows, a->first, a->count, BM, a->workspace, &route, stream);
+    if (rc) return rc;
+    const bool silu = a->stages & TS_AFTER_SILU_MUL;
+    rc = ts::zero_absent_launch(route, a->count, a->out, a->n, a->out_dtype == TS_BF16, stream);
+    if (rc) return rc;
+    TiledParams p;
+    p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = nullptr; p.out = a->out;
+    p.m = a->rows; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
+    p.perm = route.perm; p.row_start = route.row_start; p.tile_start = route.tile_start;
+    p.matrices = a->count; p.repeat = a->repeat; p.stride = a->stride; p.offset = a->offset;
+    const uint32_t cols = silu ? BN / 2 : BN;
+    // Row tiles: at most one partial tile per matrix beyond rows / BM full ones.
+    const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->rows + BM - 1) / BM + a->count;
+    Kern k = pick_kernel<true>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
+    hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
+    TS_CHECK_LAUNCH("picked launch");
     return TS_OK;
 }
 

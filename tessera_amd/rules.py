@@ -98,6 +98,74 @@ def tiled(x, w, **kw):
     return _linear("tessera_hip_tiled", x, w, **kw)
 
 
+def picked(x, w, ids, *, n=None, repeat=1, first=0, offset=0, silu_mul=False, w_scale=None, out=None,
+           out_dtype=torch.float32):
+    """Rule "picked": row r multiplies matrix ids[r] - first of the set w [count, stride, k]
+    (rows offset..offset+n, or the gate/up pair with silu_mul); x row r // repeat."""
+    count, stride, k = w.shape
+    rows = ids.numel()
+    if n is None:
+        n = (stride - offset) // 2 if silu_mul else stride - offset
+    if out is None:
+        out = torch.empty((rows, n), dtype=out_dtype, device=x.device)
+    a = abi.PickedArgs()
+    a.x, a.w, a.w_scale, a.ids, a.out = _ptr(x), _ptr(w), _ptr(w_scale), _ptr(ids), _ptr(out)
+    a.rows, a.n, a.k, a.count, a.stride, a.offset, a.repeat, a.first = rows, n, k, count, stride, offset, repeat, first
+    a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
+    a.stages = abi.TS_AFTER_SILU_MUL if silu_mul else 0
+    need = abi.load().tessera_hip_picked_workspace(C.byref(a))
+    a.workspace, a.workspace_bytes = workspace(x.device).get(need)
+    abi.call("tessera_hip_picked", C.byref(a), _stream())
+    return out
+
+
+def take(x, ids, out=None):
+    rows, width = x.shape
+    picks = ids.shape[-1]
+    if out is None:
+        out = torch.empty(ids.shape, dtype=torch.float32, device=x.device)
+    abi.call("tessera_hip_take", _ptr(x), _ptr(ids), _ptr(out), rows, width, picks, _stream())
+    return out
+
+
+def softmax(x, out=None):
+    width = x.shape[-1]
+    rows = x.numel() // width
+    if out is None:
+        out = torch.empty_like(x)
+    abi.call("tessera_hip_softmax", _ptr(x), _ptr(out), rows, width, _stream())
+    return out
+
+
+def mix(x, weights=None, out=None):
+    """Weighted sum over axis 1 of x [outer, count, inner] (mean without weights)."""
+    outer, count = x.shape[0], x.shape[1]
+    inner = x.numel() // (outer * count)
+    if out is None:
+        out = torch.empty((outer,) + tuple(x.shape[2:]), dtype=torch.float32, device=x.device)
+    abi.call("tessera_hip_mix", _ptr(x), _ptr(weights), _ptr(out), outer, count, inner, _stream())
+    return out
+
+
+def moe_layer(h, router, w_in, w_out, *, top=8, shared_in=None, shared_out=None, inner_dtype=torch.bfloat16):
+    """One MoE MLP as the reference composes it (engine/models/src/decoder.rs:73-84):
+    scores = h . router^T; ids = top_k(scores); gates = softmax(take(scores, ids));
+    inner = silu(h . gate_e) * (h . up_e) per pick; y = mix(inner . out_e, gates);
+    plus the shared expert's SwiGLU when given. Returns (y, ids, gates)."""
+    tokens = h.shape[0]
+    scores = linear(h, router)
+    ids = top_k(scores, top)
+    gates = softmax(take(scores, ids))
+    ffn = w_out.shape[2]
+    inner = picked(h, w_in, ids, n=ffn, repeat=top, silu_mul=True, out_dtype=inner_dtype)
+    y_picks = picked(inner, w_out, ids, out_dtype=torch.float32)
+    y = mix(y_picks.view(tokens, top, -1), gates)
+    if shared_in is not None:
+        s_inner = linear(h, shared_in, silu_mul=True, out_dtype=inner_dtype)
+        y = linear(s_inner, shared_out, a0=y, out=y)
+    return y, ids, gates
+
+
 def rows_args(q, k, v, out, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
               back=abi.U32_MAX, max_position=None):
     rows, heads, width = q.shape

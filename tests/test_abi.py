@@ -42,10 +42,16 @@ def test_struct_layout_matches_header():
     assert C.sizeof(abi.LinearArgs) == 8 * 8 + 4 * 8
     assert abi.LinearArgs.m.offset == 64 and abi.LinearArgs.eps.offset == 92
     assert abi.RowsArgs.rows.offset == 72 and abi.RowsArgs.max_position.offset == 120
+    assert C.sizeof(abi.PickedArgs) == 104
+    assert abi.PickedArgs.rows.offset == 56 and abi.PickedArgs.stages.offset == 100
 
 
 def test_workspace_sizes():
     lib = abi.load()
+    p = abi.PickedArgs()
+    p.rows, p.count = 4096 * 8, 128
+    # sort chunks of 256 rows x (count + 1) buckets, row starts, tile starts, the permutation
+    assert lib.tessera_hip_picked_workspace(C.byref(p)) == 4 * (128 * 129 + 130 + 129 + 4096 * 8)
     a = abi.LinearArgs()
     a.m, a.n, a.k = 1, 1024, 3072
     assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0  # nothing crosses groups
