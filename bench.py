@@ -12,6 +12,9 @@ Also measured in the same run:
   * the whole step against HBM: 1,192,099,840 weight bytes + 114,688 B per kept
     position per token;
   * prefill GEMMs (M=2048, the C2 projection shapes) as a fraction of bf16 MFMA peak;
+  * C3 paged attention (decode: 32 rows, ctx U[512, 8192]; prefill: 4 x 2048 causal),
+    C4 fp8-e4m3 weight products (M 1, 8, 64) and C5 one MoE layer, each against its
+    roofline (extra.c3_decode, c3_prefill, c4_fp8, c5_moe);
   * the CPU baseline: the oracle (a C restatement of tessera-interp) decoding a bounded
     sample of steps on this host's cores.
 """
@@ -41,6 +44,7 @@ def parse():
     p.add_argument("--cpu-steps", type=int, default=8)
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-gemm", action="store_true")
+    p.add_argument("--no-rows", action="store_true", help="skip the C3/C4/C5 measurements")
     p.add_argument("--roofline-only", action="store_true",
                    help="run only the lm_head lanes kernel and a plain copy of known size "
                         "(the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
@@ -120,6 +124,138 @@ def gemm_sweep(torch, reps=10):
     return {"M": M, "shapes": res, "aggregate_frac": round(flops_all / t_all / BF16_PEAK, 4)}
 
 
+def _graph_time(torch, fn, launches=20, replays=5):
+    """Seconds per call of fn, from a HIP graph of `launches` calls replayed `replays`
+    times (the per-node launch cost stays in; host launch overhead does not)."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(replays):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / 1e3 / (launches * replays)
+
+
+def c3_decode(torch):
+    """C3 decode: 32 rows, ctx ~ U[512, 8192] (seed 2), 16 q / 8 kv heads x 128, bf16
+    K/V in 16-row pages under a shuffled table; HBM-bound on the K/V bytes."""
+    import numpy as np
+    from tessera_amd import rules
+    r = np.random.default_rng(2)
+    rows, heads, kvh, width, page, keys = 32, 16, 8, 128, 16, 8192
+    ctx = r.integers(512, 8193, rows)
+    kept_pages = keys // page
+    table = r.permutation(rows * kept_pages).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    k = torch.randn((rows * keys, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((rows * keys, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((rows, heads, width), device="cuda", generator=g)
+    slots = torch.arange(rows, dtype=torch.int32, device="cuda")
+    pos = torch.from_numpy((ctx - 1).astype(np.int32)).cuda()
+    tab = torch.from_numpy(table).cuda()
+    out = torch.empty_like(q)
+    mp = int(ctx.max() - 1)
+    fn = lambda: rules.attend_rows(q, k, v, slots, pos, keys=keys, scale=width ** -0.5, table=tab,
+                                   kept_pages=kept_pages, page=page, max_position=mp, out=out)
+    t = _graph_time(torch, fn, launches=10)
+    nbytes = int(ctx.sum()) * kvh * width * 2 * 2 + rows * heads * width * 4 * 2 + rows * kept_pages * 4
+    return {"bound": "hbm", "us": round(t * 1e6, 2), "bytes": nbytes, "GB_s": round(nbytes / t / 1e9, 1),
+            "frac": round(nbytes / t / HBM_PEAK, 4), "sum_ctx": int(ctx.sum())}
+
+
+def c3_prefill(torch):
+    """C3 prefill: 4 sequences x 2048 causal, 16 q / 8 kv heads x 128, K/V bf16 in
+    shuffled 16-row pages; MFMA-bound: 68.75 GFLOP (causal pairs incl. the diagonal)."""
+    import numpy as np
+    from tessera_amd import rules
+    r = np.random.default_rng(4)
+    seqs, n, heads, kvh, width, page = 4, 2048, 16, 8, 128, 16
+    kept_pages = n // page
+    table = r.permutation(seqs * kept_pages).astype(np.int32)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    k = torch.randn((seqs * n, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn((seqs * n, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
+    q = torch.randn((seqs * n, heads, width), device="cuda", generator=g)
+    slots = torch.arange(seqs, dtype=torch.int32, device="cuda").repeat_interleave(n)
+    pos = torch.arange(n, dtype=torch.int32, device="cuda").repeat(seqs)
+    tab = torch.from_numpy(table).cuda()
+    out = torch.empty_like(q)
+    fn = lambda: rules.flash_rows(q, k, v, slots, pos, keys=n, scale=width ** -0.5, table=tab,
+                                  kept_pages=kept_pages, page=page, out=out)
+    t = _graph_time(torch, fn, launches=5)
+    flops = seqs * heads * (n * (n + 1) // 2) * 4 * width
+    return {"bound": "mfma", "us": round(t * 1e6, 2), "tflops": round(flops / t / 1e12, 1),
+            "frac": round(flops / t / BF16_PEAK, 4), "gflop": round(flops / 1e9, 2)}
+
+
+def c4(torch):
+    """C4: e4m3 weights with a bf16 scale per output row (absmax/448 of N(0,0.02) rows),
+    bf16 x; M in {1, 8, 64}; HBM-bound. Bytes N*K + 2N + 2MK + 2MN."""
+    from tessera_amd import rules
+    shapes = {"q_o": (4096, 4096), "k_v": (4096, 1024), "gate_up": (4096, 14336), "down": (14336, 4096)}
+    g = torch.Generator(device="cuda").manual_seed(5)
+    res, bytes_all, t_all = {}, 0.0, 0.0
+    for name, (K, N) in shapes.items():
+        w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+        scale = (w.abs().amax(1) / 448.0).to(torch.bfloat16)
+        codes = (w / scale.float()[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+        del w
+        for M in (1, 8, 64):
+            x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+            out = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+            fn = lambda: rules.linear(x, codes, w_scale=scale, out=out)
+            t = _graph_time(torch, fn, launches=20)
+            nb = N * K + 2 * N + 2 * M * K + 2 * M * N
+            res[f"{name}_M{M}"] = {"us": round(t * 1e6, 2), "frac": round(nb / t / HBM_PEAK, 4)}
+            bytes_all += nb
+            t_all += t
+    return {"bound": "hbm", "shapes": res, "aggregate_frac": round(bytes_all / t_all / HBM_PEAK, 4)}
+
+
+def c5(torch):
+    """C5: one MoE layer, 4096 tokens, hidden 4096, 128 experts top-8 (softmax over the
+    8 picked logits), FFN 1536, plus one shared expert; gate logits N(0,1) f32 (seed 3).
+    Roofline max(557 us MFMA, 609 us HBM) = 0.609 ms."""
+    from tessera_amd import rules
+    tokens, hidden, experts, top, ffn = 4096, 4096, 128, 8, 1536
+    g = torch.Generator(device="cuda").manual_seed(3)
+    logits = torch.randn((tokens, experts), device="cuda", generator=g)
+    h = torch.randn((tokens, hidden), device="cuda", generator=g).to(torch.bfloat16)
+    w_in = torch.empty((experts, 2 * ffn, hidden), device="cuda", dtype=torch.bfloat16)
+    w_out = torch.empty((experts, hidden, ffn), device="cuda", dtype=torch.bfloat16)
+    for e in range(experts):  # N(0, 0.02) per expert, keeping the f32 temporaries small
+        w_in[e] = (torch.randn((2 * ffn, hidden), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        w_out[e] = (torch.randn((hidden, ffn), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    s_in = (torch.randn((2 * ffn, hidden), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    s_out = (torch.randn((hidden, ffn), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    fn = lambda: rules.moe_layer(h, None, w_in, w_out, top=top, shared_in=s_in, shared_out=s_out, scores=logits)
+    fn()
+    torch.cuda.synchronize()
+    reps = 3
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    t = s.elapsed_time(e) / 1e3 / reps
+    flops = 2.0 * (tokens * top + tokens) * 3 * hidden * ffn
+    wbytes = (experts + 1) * 3 * hidden * ffn * 2
+    roof = max(flops / BF16_PEAK, wbytes / HBM_PEAK)
+    del w_in, w_out
+    return {"bound": "balanced", "ms": round(t * 1e3, 3), "tflops": round(flops / t / 1e12, 1),
+            "weight_GB_s": round(wbytes / t / 1e9, 1), "roofline_ms": round(roof * 1e3, 3),
+            "frac": round(roof / t, 4)}
+
+
 def cpu_baseline(model, prompt, steps):
     """The oracle decoding `steps` tokens after the same prompt, kept rows copied from
     the device after its prefill; all host cores (up to 16) via OpenMP."""
@@ -191,6 +327,13 @@ def main():
     cpu = None
     if not a.no_cpu and a.cpu_steps > 0:
         cpu = cpu_baseline(m, prompt, a.cpu_steps)
+    m.close()
+    if not a.no_rows:
+        torch.cuda.empty_cache()
+        extra["c3_decode"] = c3_decode(torch)
+        extra["c3_prefill"] = c3_prefill(torch)
+        extra["c4_fp8"] = c4(torch)
+        extra["c5_moe"] = c5(torch)
     line = {
         "metric": "decode tok/s + % HBM roofline (Qwen3-0.6B-shape b=1); prefill GEMM % MFMA peak",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
@@ -202,7 +345,6 @@ def main():
         "roofline": roof, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line), flush=True)
-    m.close()
 
 
 if __name__ == "__main__":

@@ -78,13 +78,17 @@ typedef struct {
     float eps;            /* RmsNorm epsilon */
 } ts_linear_args;
 
-/* Picks `lanes` for m <= 16 and `tiled` otherwise (the cost select of
+/* Picks `lanes` for m <= 64 and `tiled` otherwise (the cost select of
  * engine/plan/lower/src/cost.rs between the two rules). */
 int tessera_hip_linear(const ts_linear_args *a, void *stream);
 size_t tessera_hip_linear_workspace(const ts_linear_args *a);
 
-/* Few rows (m <= 16): a wave per 16 output columns on the matrix unit, weights
- * streamed once with 64-byte runs per lane, split-K across waves and groups.
+/* Few rows (m <= 64): m <= 4 on the vector ALU (a wave streams whole weight
+ * rows); 5..64 on the matrix unit: a wave per 16 output columns, x staged once
+ * per group in LDS, weights streamed once with 64-byte runs per lane, k split
+ * across groups when the columns alone do not cover the chip (partials in the
+ * workspace, summed in split order by a second kernel: deterministic).
+ * TS_BEFORE_RMS_NORM needs f32 x and m <= 16.
  * Replaces: rule "lanes" (engine/rules/linear/src/lanes.rs:17-143) and "thin"
  * (engine/rules/linear/src/thin.rs:11-104). */
 int tessera_hip_lanes(const ts_linear_args *a, void *stream);

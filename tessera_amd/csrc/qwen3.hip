@@ -23,6 +23,8 @@
 #include "../../include/tessera_run.h"
 #include "common.h"
 
+#include <algorithm>
+
 namespace {
 
 // splitmix64: a counter-based hash, so every weight element is a pure function
@@ -224,12 +226,16 @@ size_t workspace_need(ts_qwen3 *m) {
     const uint32_t H = c.hidden, D = c.head_dim;
     const uint32_t shapes[][2] = {{(c.heads + 2 * c.kv_heads) * D, H}, {H, c.heads * D}, {c.ffn, H},
                                   {H, c.ffn}, {c.vocab, H}};
-    for (auto &sh : shapes) {
-        ts_linear_args a = lin(nullptr, nullptr, nullptr, 1, sh[0], sh[1], m);
-        if (sh[0] == c.ffn && sh[1] == H) a.stages = TS_AFTER_SILU_MUL;
-        size_t w = tessera_hip_linear_workspace(&a);
-        if (w > need) need = w;
-    }
+    // Split partials grow with the rows: size for one row and for the most rows a
+    // launch can carry to the few-row kernels (up to 64).
+    const uint32_t row_counts[] = {1, std::min<uint32_t>(c.max_prompt, 64)};
+    for (uint32_t rows : row_counts)
+        for (auto &sh : shapes) {
+            ts_linear_args a = lin(nullptr, nullptr, nullptr, rows, sh[0], sh[1], m);
+            if (sh[0] == c.ffn && sh[1] == H) a.stages = TS_AFTER_SILU_MUL;
+            size_t w = tessera_hip_linear_workspace(&a);
+            if (w > need) need = w;
+        }
     Layer L{};
     ts_rows_args r = rows_args(m, L, 1, nullptr, nullptr, c.max_context - 1);
     size_t w = tessera_hip_attend_rows_workspace(&r);

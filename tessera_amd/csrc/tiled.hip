@@ -351,10 +351,10 @@ extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
 
 extern "C" size_t tessera_hip_linear_workspace(const ts_linear_args *a) {
     if (!a) return 0;
-    return a->m <= 16 ? tessera_hip_lanes_workspace(a) : 0;
+    return a->m <= 64 ? tessera_hip_lanes_workspace(a) : 0;
 }
 
 extern "C" int tessera_hip_linear(const ts_linear_args *a, void *stream) {
     TS_REQUIRE(a, "linear: null args");
-    return a->m <= 16 ? tessera_hip_lanes(a, stream) : tessera_hip_tiled(a, stream);
+    return a->m <= 64 ? tessera_hip_lanes(a, stream) : tessera_hip_tiled(a, stream);
 }

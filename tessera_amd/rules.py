@@ -89,7 +89,7 @@ def linear(x, w, **kw):
 
 
 def lanes(x, w, **kw):
-    """Few-row product (rule "lanes"/"thin"): m <= 16."""
+    """Few-row product (rule "lanes"/"thin"): m <= 64."""
     return _linear("tessera_hip_lanes", x, w, **kw)
 
 
@@ -147,13 +147,16 @@ def mix(x, weights=None, out=None):
     return out
 
 
-def moe_layer(h, router, w_in, w_out, *, top=8, shared_in=None, shared_out=None, inner_dtype=torch.bfloat16):
+def moe_layer(h, router, w_in, w_out, *, top=8, shared_in=None, shared_out=None, inner_dtype=torch.bfloat16,
+              scores=None):
     """One MoE MLP as the reference composes it (engine/models/src/decoder.rs:73-84):
     scores = h . router^T; ids = top_k(scores); gates = softmax(take(scores, ids));
     inner = silu(h . gate_e) * (h . up_e) per pick; y = mix(inner . out_e, gates);
-    plus the shared expert's SwiGLU when given. Returns (y, ids, gates)."""
+    plus the shared expert's SwiGLU when given. `scores` given: the router product is
+    skipped (router may be None). Returns (y, ids, gates)."""
     tokens = h.shape[0]
-    scores = linear(h, router)
+    if scores is None:
+        scores = linear(h, router)
     ids = top_k(scores, top)
     gates = softmax(take(scores, ids))
     ffn = w_out.shape[2]

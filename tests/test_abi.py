@@ -26,9 +26,9 @@ def test_argument_errors_need_no_device():
     assert lib.tessera_hip_lanes(C.byref(a), None) == abi.TS_ERR_ARG
     assert b"null" in lib.tessera_hip_last_error()
     a.x = a.w = a.out = 16
-    a.m, a.n, a.k = 17, 8, 64
+    a.m, a.n, a.k = 65, 8, 64
     assert lib.tessera_hip_lanes(C.byref(a), None) == abi.TS_ERR_ARG
-    assert b"m=17" in lib.tessera_hip_last_error()
+    assert b"m=65" in lib.tessera_hip_last_error()
     r = abi.RowsArgs()
     r.q = r.k = r.v = r.out = r.slots = r.positions = 16
     r.width, r.heads, r.kv_heads = 64, 16, 8
@@ -54,7 +54,12 @@ def test_workspace_sizes():
     assert lib.tessera_hip_picked_workspace(C.byref(p)) == 4 * (128 * 129 + 130 + 129 + 4096 * 8)
     a = abi.LinearArgs()
     a.m, a.n, a.k = 1, 1024, 3072
-    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0  # nothing crosses groups
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0  # m <= 4: the vector-ALU kernel, no split
+    a.m, a.n, a.k = 64, 1024, 4096
+    # 16 column groups of 64; k split 32 ways (one 128-deep chunk each): raw f32 sums
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 32 * 64 * 1024 * 4
+    a.m, a.n, a.k = 8, 14336, 4096
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 3 * 8 * 14336 * 4
     r = abi.RowsArgs()
     r.rows, r.heads, r.kv_heads, r.width = 32, 16, 8, 128
     r.max_position = 150

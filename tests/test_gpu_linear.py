@@ -151,8 +151,8 @@ def test_e4m3_weights(m):
 def test_argument_errors_raise():
     R = _rules()
     from tessera_amd import abi
-    x = torch.zeros((17, 64), device="cuda")
+    x = torch.zeros((65, 64), device="cuda")
     w = torch.zeros((8, 64), device="cuda", dtype=torch.bfloat16)
     with pytest.raises(abi.HipError) as e:
         R.lanes(x, w)
-    assert e.value.code == abi.TS_ERR_ARG and "m=17" in str(e.value)
+    assert e.value.code == abi.TS_ERR_ARG and "m=65" in str(e.value)
