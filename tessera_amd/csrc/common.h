@@ -93,11 +93,20 @@ TS_DEV float e4m3_float(uint32_t c) {
 }
 
 // Four e4m3 codes (one u32) -> two packed bf16 pairs (exact: 3 mantissa bits).
+// Four e4m3 codes (OCP e4m3fn: bias 7, subnormals, NaN 0x7f/0xff) to four bf16, in
+// byte order, with the gfx950 conversion (scale 1.0): every e4m3 value is exact in bf16.
 TS_DEV u32x2 e4m3x4_to_bf16x4(uint32_t w) {
-    u32x2 r;
-    r.x = pack_bf16x2(e4m3_float(w & 0xff), e4m3_float((w >> 8) & 0xff));
-    r.y = pack_bf16x2(e4m3_float((w >> 16) & 0xff), e4m3_float(w >> 24));
-    return r;
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    const bf16x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    return u32x2{__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+}
+
+// Four e4m3 codes to f32, in byte order (gfx950 v_cvt_pk_f32_fp8; exact).
+TS_DEV void e4m3x4_to_f32(uint32_t w, float *f) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+    f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
 }
 
 // ---------------------------------------------------------------------------
@@ -160,6 +169,12 @@ TS_DEV f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 // D = A * B^T + C on a 32 x 32 x 16 tile. A lane l: row l % 32, k 8 (l / 32) .. +7;
 // B likewise by column; D lane l: column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4.
 TS_DEV f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) { return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0); }
+
+// A group barrier that publishes LDS writes (lgkmcnt(0)) but leaves global loads in
+// flight. __syncthreads() also fences global memory, which makes the compiler wait
+// for every outstanding load (vmcnt(0)) first and drains any prefetch. The memory
+// clobber keeps the compiler from moving LDS accesses across it.
+TS_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 TS_DEV bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -52,11 +52,10 @@ TS_DEV void widen_w(u32x4 v, float (&f)[W8 ? 16 : 8]) {
         f[0] = lo_bf16(v.x); f[1] = hi_bf16(v.x); f[2] = lo_bf16(v.y); f[3] = hi_bf16(v.y);
         f[4] = lo_bf16(v.z); f[5] = hi_bf16(v.z); f[6] = lo_bf16(v.w); f[7] = hi_bf16(v.w);
     } else {
-        const uint32_t c[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) f[4 * i + e] = e4m3_float((c[i] >> (8 * e)) & 0xff);
+        e4m3x4_to_f32(v.x, f);
+        e4m3x4_to_f32(v.y, f + 4);
+        e4m3x4_to_f32(v.z, f + 8);
+        e4m3x4_to_f32(v.w, f + 12);
     }
 }
 

@@ -9,10 +9,10 @@
 // and the chip must be covered. A wave owns 16 output columns; a group of 4 waves
 // (64 columns) shares each 128-deep chunk of x, staged once in LDS (double-
 // buffered) as MFMA A fragments for up to 4 row tiles of 16. Each lane streams 64
-// contiguous bytes of its column's weight row per chunk (16B vector loads; lane
-// group g holds k [32g, 32g+32)), fetched one chunk ahead, and feeds them to
+// bytes of its column's weight row per chunk (16B vector loads; the 4 lanes of a row
+// read contiguous runs), a ring of chunks ahead, and feeds them to
 // v_mfma_f32_16x16x32_bf16 straight from registers (no LDS for the weights). The x
-// fragments use the same k assignment, so the product is unchanged. When the
+// fragments use the same k permutation, so the product is unchanged. When the
 // column groups alone do not give ~512 groups, k is split across groups: raw sums
 // go to the caller's workspace and a second kernel adds the splits in split order
 // (deterministic) before the epilogue. f32 activations are split into two exact
@@ -41,87 +41,136 @@ struct LanesParams {
     int out_bf16;
 };
 
-// Weight chunk for one lane: 32 consecutive k of one row as bf16 (4 x 16B).
+// Raw weight bytes of one lane (row `row`, lane group g) for the 128-deep chunk at
+// k0, laid out so the 4 lanes of a row read contiguous runs: bf16 b[j] = k [32j + 8g,
+// +8) (each load instruction covers 64 contiguous bytes per row); e4m3 b[h] = k [64h +
+// 16g, +16) (h = 0, 1). Decoded at use by w_frag, so the loads stay in flight.
+// `full` (uniform per chunk): the chunk lies inside K and rows are 16-byte aligned;
+// otherwise element loads zero-fill past K.
 template <bool W8>
-TS_DEV void load_w(const void *w, uint32_t row, uint32_t nrows, uint32_t k0, uint32_t K, u32x4 (&b)[4]) {
-    if (row >= nrows) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) b[j] = u32x4{0, 0, 0, 0};
-        return;
-    }
+TS_DEV void load_w(const void *w, uint32_t row, uint32_t k0, uint32_t g, uint32_t K, bool full, u32x4 (&b)[4]) {
     if (!W8) {
-        const uint16_t *p = (const uint16_t *)w + (size_t)row * K + k0;
-        if (k0 + 32 <= K && (K % 8) == 0) {
-            const u32x4 *q = (const u32x4 *)p;
+        const uint16_t *p = (const uint16_t *)w + (size_t)row * K;
 #pragma unroll
-            for (int j = 0; j < 4; j++) b[j] = __builtin_nontemporal_load(q + j);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
+        for (int j = 0; j < 4; j++) {
+            const uint32_t k = k0 + 32 * j + 8 * g;
+            if (full) {
+                b[j] = __builtin_nontemporal_load((const u32x4 *)(p + k));
+            } else {
                 uint32_t v[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    uint32_t ka = k0 + 8 * j + 2 * e;
-                    uint32_t lo = ka < K ? p[8 * j + 2 * e] : 0u;
-                    uint32_t hi = ka + 1 < K ? p[8 * j + 2 * e + 1] : 0u;
-                    v[e] = lo | (hi << 16);
-                }
+                for (int e = 0; e < 4; e++)
+                    v[e] = (k + 2 * e < K ? (uint32_t)p[k + 2 * e] : 0u) | ((k + 2 * e + 1 < K ? (uint32_t)p[k + 2 * e + 1] : 0u) << 16);
                 b[j] = u32x4{v[0], v[1], v[2], v[3]};
             }
         }
     } else {
-        const uint8_t *p = (const uint8_t *)w + (size_t)row * K + k0;
-        uint32_t c[8];
-        if (k0 + 32 <= K && (K % 16) == 0) {
-            const u32x4 *q = (const u32x4 *)p;
-            u32x4 c0 = __builtin_nontemporal_load(q), c1 = __builtin_nontemporal_load(q + 1);
-            c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w;
-            c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
-        } else {
+        const uint8_t *p = (const uint8_t *)w + (size_t)row * K;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                uint32_t v = 0;
+        for (int h = 0; h < 2; h++) {
+            const uint32_t k = k0 + 64 * h + 16 * g;
+            if (full) {
+                b[h] = __builtin_nontemporal_load((const u32x4 *)(p + k));
+            } else {
+                uint32_t c[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    uint32_t ka = k0 + 4 * i + e;
-                    v |= (ka < K ? (uint32_t)p[4 * i + e] : 0u) << (8 * e);
+                for (int i = 0; i < 4; i++) {
+                    uint32_t v = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v |= (k + 4 * i + e < K ? (uint32_t)p[k + 4 * i + e] : 0u) << (8 * e);
+                    c[i] = v;
                 }
-                c[i] = v;
+                b[h] = u32x4{c[0], c[1], c[2], c[3]};
             }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            u32x2 a = e4m3x4_to_bf16x4(c[2 * j]), d = e4m3x4_to_bf16x4(c[2 * j + 1]);
-            b[j] = u32x4{a.x, a.y, d.x, d.y};
         }
     }
 }
 
+// MFMA B fragment j of a raw chunk: 8 k values of this lane.
+template <bool W8>
+TS_DEV bf16x8 w_frag(const u32x4 (&b)[4], int j) {
+    if (!W8) return as_bf16x8(b[j]);
+    const u32x4 q = b[j >> 1];
+    const uint32_t lo = (j & 1) ? q.z : q.x, hi = (j & 1) ? q.w : q.y;
+    const u32x2 a = e4m3x4_to_bf16x4(lo), d = e4m3x4_to_bf16x4(hi);
+    return as_bf16x8(u32x4{a.x, a.y, d.x, d.y});
+}
+
+// The 16-byte piece (8 k values) of an x row chunk that pairs with w_frag j of lane
+// group g: bf16 weights k [32j + 8g, +8); e4m3 k [64 (j/2) + 16g + 8 (j%2), +8).
+template <bool W8>
+TS_DEV uint32_t x_piece(int j, uint32_t g) {
+    return W8 ? 8 * (j >> 1) + 2 * g + (j & 1) : 4 * j + g;
+}
+
 TS_DEV float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// One 128-deep chunk of x rows [0, M) into LDS as bf16 (hi, and lo for f32 rows:
-// hi = bf16(x), lo = bf16(x - hi)), rows of 256 bytes with 16-byte chunks XOR-swizzled
-// by row. Rows >= M and k >= K are zero. NORM scales f32 rows by inv[m] * gain[k].
-template <int MT, bool XF32, bool NORM>
-TS_DEV void stage_x(const LanesParams &p, const float *inv, uint32_t k0, char *hi, char *lo) {
-    constexpr uint32_t kRows = 16 * MT, kPieces = kRows * (kChunk / 8);  // 8 k values per piece
+// One 128-deep chunk of x rows [0, M) in flight: thread t holds pieces i = t + 256 j
+// (piece = 8 k values of one row; 16 pieces per row). Loaded early into registers,
+// written to LDS later (store_x), so the load latency hides under the MFMAs.
+template <int MT, bool XF32>
+struct XRegs {
+    static constexpr uint32_t kPieces = 16 * MT * (kChunk / 8), kPer = kPieces / (kWaves * 64);
+    float4 f[XF32 ? 2 * kPer : 1];
+    u32x4 b[XF32 ? 1 : kPer];
+};
+
+// Rows past M repeat row M - 1 (their products are never stored). `full` (uniform):
+// the chunk lies inside K and rows are 16-byte aligned.
+template <int MT, bool XF32>
+TS_DEV void load_x(const LanesParams &p, uint32_t k0, bool full, XRegs<MT, XF32> &r) {
     const uint32_t M = p.m, K = p.k;
-    for (uint32_t i = threadIdx.x; i < kPieces; i += kWaves * 64) {
-        const uint32_t m = i / (kChunk / 8), c = i % (kChunk / 8), k = k0 + 8 * c;
+#pragma unroll
+    for (uint32_t j = 0; j < XRegs<MT, XF32>::kPer; j++) {
+        const uint32_t i = threadIdx.x + j * kWaves * 64, k = k0 + 8 * (i % (kChunk / 8));
+        const uint32_t m = min(i / (kChunk / 8), M - 1);
+        if (XF32) {
+            if (full) {
+                const float4 *q = (const float4 *)((const float *)p.x + (size_t)m * K + k);
+                r.f[2 * j] = q[0];
+                r.f[2 * j + 1] = q[1];
+            } else {
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = k + e < K ? ((const float *)p.x)[(size_t)m * K + k + e] : 0.0f;
+                r.f[2 * j] = float4{v[0], v[1], v[2], v[3]};
+                r.f[2 * j + 1] = float4{v[4], v[5], v[6], v[7]};
+            }
+        } else {
+            u32x4 v;
+            if (full) {
+                v = *(const u32x4 *)((const uint16_t *)p.x + (size_t)m * K + k);
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint16_t *q = (const uint16_t *)p.x + (size_t)m * K + k + 2 * e;
+                    w[e] = (k + 2 * e < K ? (uint32_t)q[0] : 0u) | ((k + 2 * e + 1 < K ? (uint32_t)q[1] : 0u) << 16);
+                }
+                v = u32x4{w[0], w[1], w[2], w[3]};
+            }
+            r.b[j] = v;
+        }
+    }
+}
+
+// The chunk into LDS as bf16 (hi, and lo for f32 rows: hi = bf16(x), lo = bf16(x -
+// hi)), rows of 256 bytes with 16-byte pieces XOR-swizzled by row. NORM scales f32
+// rows by inv[m] * gain[k].
+template <int MT, bool XF32, bool NORM>
+TS_DEV void store_x(const LanesParams &p, const float *inv, uint32_t k0, const XRegs<MT, XF32> &r, char *hi,
+                    char *lo) {
+#pragma unroll
+    for (uint32_t j = 0; j < XRegs<MT, XF32>::kPer; j++) {
+        const uint32_t i = threadIdx.x + j * kWaves * 64, m = i / (kChunk / 8), c = i % (kChunk / 8);
         const uint32_t at = m * 256 + ((c ^ (m & 15)) << 4);
         if (XF32) {
-            float v[8];
-            if (m < M && k + 8 <= K) {
-                const float4 *q = (const float4 *)((const float *)p.x + (size_t)m * K + k);
-                const float4 u0 = q[0], u1 = q[1];
-                v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w; v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
-            } else {
+            const float4 u0 = r.f[2 * j], u1 = r.f[2 * j + 1];
+            float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+            if (NORM && m < p.m) {
+                const uint32_t k = k0 + 8 * c;
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (m < M && k + e < K) ? ((const float *)p.x)[(size_t)m * K + k + e] : 0.0f;
-            }
-            if (NORM && m < M) {
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] *= inv[m] * (k + e < K ? p.gain[k + e] : 0.0f);
+                for (int e = 0; e < 8; e++) v[e] *= inv[m] * (k + e < p.k ? p.gain[k + e] : 0.0f);
             }
             uint32_t h[4], l[4];
 #pragma unroll
@@ -133,31 +182,21 @@ TS_DEV void stage_x(const LanesParams &p, const float *inv, uint32_t k0, char *h
             *(u32x4 *)(hi + at) = u32x4{h[0], h[1], h[2], h[3]};
             *(u32x4 *)(lo + at) = u32x4{l[0], l[1], l[2], l[3]};
         } else {
-            u32x4 v = {0, 0, 0, 0};
-            if (m < M && k + 8 <= K) {
-                v = *(const u32x4 *)((const uint16_t *)p.x + (size_t)m * K + k);
-            } else if (m < M) {
-                uint32_t w[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint16_t *q = (const uint16_t *)p.x + (size_t)m * K + k + 2 * e;
-                    w[e] = (k + 2 * e < K ? (uint32_t)q[0] : 0u) | ((k + 2 * e + 1 < K ? (uint32_t)q[1] : 0u) << 16);
-                }
-                v = u32x4{w[0], w[1], w[2], w[3]};
-            }
-            *(u32x4 *)(hi + at) = v;
+            *(u32x4 *)(hi + at) = r.b[j];
         }
     }
 }
 
 // Few rows (m <= 64): wave w of group (tile group gx, split s) owns output columns
 // [16 (4 gx + w), +16) over the chunks of split s. Each 128-deep chunk of x is staged
-// in LDS once per group (double-buffered) and read as MFMA A fragments; each lane
-// streams 64 bytes of its column's weight row per chunk (lane group g: k [32g, 32g +
-// 32)), fetched one chunk ahead. splits == 1: the epilogue runs here; otherwise the
-// raw sums go to part[s][SILU ? 2 : 1][m][n] for lanes_finish.
+// in LDS once per group (double-buffered; its global loads are issued a chunk early)
+// and read as MFMA A fragments. Each lane streams 64 bytes of its column's weight row
+// per chunk (the 4 lanes of a row read contiguous runs, see load_w) into a register
+// ring D chunks deep, so D chunks of weights are in flight per wave. splits == 1: the epilogue runs here;
+// otherwise the raw sums go to part[s][SILU ? 2 : 1][m][n] for lanes_finish.
 template <int MT, bool XF32, bool W8, bool SILU, bool NORM>
 __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float *part) {
+    constexpr int D = (SILU && !W8) ? 2 : 4;     // weight chunks in flight per wave
     constexpr uint32_t kXBytes = 16 * MT * 256;  // one chunk of x rows, bf16
     __shared__ __attribute__((aligned(16))) char xs[2][XF32 ? 2 : 1][kXBytes];
     __shared__ float inv_s[16 * MT];
@@ -168,13 +207,35 @@ __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float
     const uint32_t n0 = (blockIdx.x * kWaves + wave) * 16, M = p.m, N = p.n, K = p.k;
     const uint32_t split = blockIdx.y, splits = gridDim.y;
 
+    const uint32_t chunks = (K + kChunk - 1) / kChunk;
+    const uint32_t cb = (uint32_t)(((uint64_t)chunks * split) / splits);
+    const uint32_t ce = (uint32_t)(((uint64_t)chunks * (split + 1)) / splits);
+
+    // Columns past N read row N - 1 (never stored). A chunk is `full` when it lies
+    // inside K and rows are 16-byte aligned (uniform: no per-lane branches).
+    const uint32_t wrow = min(n0 + col, N - 1);
+    const bool w_aligned = W8 ? (K % 16) == 0 : (K % 8) == 0, x_aligned = XF32 ? (K % 4) == 0 : (K % 8) == 0;
+    auto w_full = [&](uint32_t c) { return w_aligned && (c + 1) * kChunk <= K; };
+    auto x_full = [&](uint32_t c) { return x_aligned && (c + 1) * kChunk <= K; };
+
+    // Weights first: they are the HBM stream.
+    u32x4 wg[D][4], wu[D][4];
+#pragma unroll
+    for (int d = 0; d < D; d++)
+        if (cb + d < ce) {
+            load_w<W8>(p.w, wrow, (cb + d) * kChunk, grp, K, w_full(cb + d), wg[d]);
+            if (SILU) load_w<W8>(p.w, N + wrow, (cb + d) * kChunk, grp, K, w_full(cb + d), wu[d]);
+        }
+    XRegs<MT, XF32> xr;
+    if (cb < ce) load_x<MT, XF32>(p, cb * kChunk, x_full(cb), xr);
+
     // Fused RmsNorm prologue (f32 rows): every group computes the same inverse roots
     // in the same order, so all groups agree bit for bit.
     if (NORM) {
         for (uint32_t m = 0; m < M; m++) {
-            const float *xr = (const float *)p.x + (size_t)m * K;
+            const float *xrow = (const float *)p.x + (size_t)m * K;
             float s = 0.0f;
-            for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) s += xr[i] * xr[i];
+            for (uint32_t i = threadIdx.x; i < K; i += blockDim.x) s += xrow[i] * xrow[i];
             s = wave_sum(s);
             if (lane == 0) part_s[wave][m] = s;
         }
@@ -187,53 +248,40 @@ __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float
         __syncthreads();
     }
 
-    const uint32_t chunks = (K + kChunk - 1) / kChunk;
-    const uint32_t cb = (uint32_t)(((uint64_t)chunks * split) / splits);
-    const uint32_t ce = (uint32_t)(((uint64_t)chunks * (split + 1)) / splits);
-
     f32x4 acc_g[MT], acc_u[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc_g[t] = acc_u[t] = f32x4{0, 0, 0, 0};
-    u32x4 bg[4], bu[4];
-    if (cb < ce) {
-        stage_x<MT, XF32, NORM>(p, inv_s, cb * kChunk, xs[0][0], xs[0][XF32 ? 1 : 0]);
-        load_w<W8>(p.w, n0 + col, N, cb * kChunk + 32 * grp, K, bg);
-        if (SILU) load_w<W8>(p.w, N + n0 + col, 2 * N, cb * kChunk + 32 * grp, K, bu);
-    }
-    __syncthreads();
-    for (uint32_t c = cb; c < ce; c++) {
-        const uint32_t cur = (c - cb) & 1;
-        u32x4 ng[4], nu[4];
-        if (c + 1 < ce) {  // next chunk: weights into registers, x into the other buffer
-            load_w<W8>(p.w, n0 + col, N, (c + 1) * kChunk + 32 * grp, K, ng);
-            if (SILU) load_w<W8>(p.w, N + n0 + col, 2 * N, (c + 1) * kChunk + 32 * grp, K, nu);
-            stage_x<MT, XF32, NORM>(p, inv_s, (c + 1) * kChunk, xs[cur ^ 1][0], xs[cur ^ 1][XF32 ? 1 : 0]);
-        }
-        const char *xh = xs[cur][0], *xl = xs[cur][XF32 ? 1 : 0];
+    for (uint32_t c = cb; c < ce; c += D) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t xc = 4 * grp + j;  // 16-byte piece of the chunk: k 32 grp + 8 j
-#pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const uint32_t m = 16 * t + col;
-                const bf16x8 ah = as_bf16x8(*(const u32x4 *)(xh + m * 256 + ((xc ^ (m & 15)) << 4)));
-                acc_g[t] = mfma16(ah, as_bf16x8(bg[j]), acc_g[t]);
-                if (SILU) acc_u[t] = mfma16(ah, as_bf16x8(bu[j]), acc_u[t]);
-                if (XF32) {
-                    const bf16x8 al = as_bf16x8(*(const u32x4 *)(xl + m * 256 + ((xc ^ (m & 15)) << 4)));
-                    acc_g[t] = mfma16(al, as_bf16x8(bg[j]), acc_g[t]);
-                    if (SILU) acc_u[t] = mfma16(al, as_bf16x8(bu[j]), acc_u[t]);
-                }
-            }
-        }
-        if (c + 1 < ce) {
+        for (int u = 0; u < D; u++) {
+            const uint32_t cc = c + u;
+            if (cc >= ce) break;
+            char *xh = xs[cc & 1][0], *xl = xs[cc & 1][XF32 ? 1 : 0];
+            // Buffer cc & 1 was last read before the previous barrier.
+            store_x<MT, XF32, NORM>(p, inv_s, cc * kChunk, xr, xh, xl);
+            if (cc + 1 < ce) load_x<MT, XF32>(p, (cc + 1) * kChunk, x_full(cc + 1), xr);
+            lds_barrier();  // x of chunk cc is in LDS; the weight ring stays in flight
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                bg[j] = ng[j];
-                if (SILU) bu[j] = nu[j];
+                const uint32_t xc = x_piece<W8>(j, grp);
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const uint32_t m = 16 * t + col;
+                    const bf16x8 ah = as_bf16x8(*(const u32x4 *)(xh + m * 256 + ((xc ^ (m & 15)) << 4)));
+                    acc_g[t] = mfma16(ah, w_frag<W8>(wg[u], j), acc_g[t]);
+                    if (SILU) acc_u[t] = mfma16(ah, w_frag<W8>(wu[u], j), acc_u[t]);
+                    if (XF32) {
+                        const bf16x8 al = as_bf16x8(*(const u32x4 *)(xl + m * 256 + ((xc ^ (m & 15)) << 4)));
+                        acc_g[t] = mfma16(al, w_frag<W8>(wg[u], j), acc_g[t]);
+                        if (SILU) acc_u[t] = mfma16(al, w_frag<W8>(wu[u], j), acc_u[t]);
+                    }
+                }
+            }
+            if (cc + D < ce) {  // refill this ring slot D chunks ahead
+                load_w<W8>(p.w, wrow, (cc + D) * kChunk, grp, K, w_full(cc + D), wg[u]);
+                if (SILU) load_w<W8>(p.w, N + wrow, (cc + D) * kChunk, grp, K, w_full(cc + D), wu[u]);
             }
         }
-        __syncthreads();
     }
 
     // D lane layout: column col, rows 4 grp + r of each 16-row tile.

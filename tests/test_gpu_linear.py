@@ -156,3 +156,23 @@ def test_argument_errors_raise():
     with pytest.raises(abi.HipError) as e:
         R.lanes(x, w)
     assert e.value.code == abi.TS_ERR_ARG and "m=65" in str(e.value)
+
+
+@pytest.mark.parametrize("m", [1, 8, 80])
+def test_e4m3_decode_every_code(m):
+    """Every e4m3 code through the product paths (vector ALU m=1, few-row MFMA m=8,
+    tiled m=80): row n holds code n everywhere, scale 1.0, x = one-hot at k=0, so
+    out[:, n] is the decoded code itself; bit-exact against the oracle's e4m3 widen
+    (scalar.rs), NaN for 0x7f/0xff (-0 compares equal to the +0 a sum from 0 gives)."""
+    R = _rules()
+    k = 64
+    codes = np.repeat(np.arange(256, dtype=np.uint8)[:, None], k, axis=1)
+    scale = O.bf16_narrow(np.ones(256, np.float32))
+    x = np.zeros((m, k), np.float32)
+    x[:, 0] = 1.0
+    got = from_dev(R.linear(to_dev(x, torch), to_dev(codes, torch), w_scale=to_dev(scale, torch)))
+    want = O.e4m3_widen(np.arange(256, dtype=np.uint8))
+    for row in got:
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(row), nan)
+        assert np.array_equal(row[~nan], want[~nan].astype(np.float32))
