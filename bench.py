@@ -172,8 +172,9 @@ def c3_decode(torch):
 
 
 def c3_prefill(torch):
-    """C3 prefill: 4 sequences x 2048 causal, 16 q / 8 kv heads x 128, K/V bf16 in
-    shuffled 16-row pages; MFMA-bound: 68.75 GFLOP (causal pairs incl. the diagonal)."""
+    """C3 prefill: 4 sequences x 2048 causal, 16 q / 8 kv heads x 128, q and K/V bf16
+    (K/V in shuffled 16-row pages), f32 out; MFMA-bound: 68.75 GFLOP (causal pairs
+    incl. the diagonal)."""
     import numpy as np
     from tessera_amd import rules
     r = np.random.default_rng(4)
@@ -183,11 +184,11 @@ def c3_prefill(torch):
     g = torch.Generator(device="cuda").manual_seed(4)
     k = torch.randn((seqs * n, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
     v = torch.randn((seqs * n, kvh, width), device="cuda", generator=g).to(torch.bfloat16)
-    q = torch.randn((seqs * n, heads, width), device="cuda", generator=g)
+    q = torch.randn((seqs * n, heads, width), device="cuda", generator=g).to(torch.bfloat16)
     slots = torch.arange(seqs, dtype=torch.int32, device="cuda").repeat_interleave(n)
     pos = torch.arange(n, dtype=torch.int32, device="cuda").repeat(seqs)
     tab = torch.from_numpy(table).cuda()
-    out = torch.empty_like(q)
+    out = torch.empty(q.shape, device="cuda")
     fn = lambda: rules.flash_rows(q, k, v, slots, pos, keys=n, scale=width ** -0.5, table=tab,
                                   kept_pages=kept_pages, page=page, out=out)
     t = _graph_time(torch, fn, launches=5)

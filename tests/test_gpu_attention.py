@@ -103,6 +103,31 @@ def test_prefill_flash_rows(lens):
     np.testing.assert_allclose(run("flash", c, s), want(c, s), atol=ATOL, rtol=0)
 
 
+@pytest.mark.parametrize("lens", [[130, 70], [2048]])
+def test_prefill_flash_rows_bf16_q(lens):
+    """bf16 q (the C3 prefill form): q single-part on the matrix unit, P rounded once
+    to bf16. The oracle reads the same bf16 q widened; the one P rounding bounds the
+    error by 2^-9 * max|v| per output: atol 4e-3."""
+    from tessera_amd import rules as R
+    slots, positions = [], []
+    for s_, n in enumerate(lens):
+        slots += [s_] * n
+        positions += list(range(n))
+        pad = (-n) % 64
+        if s_ + 1 < len(lens) and pad:
+            slots += [s_] * pad
+            positions += [n - 1] * pad
+    c = paged_case(sum(lens) + 1, lens, pos=(slots, positions))
+    qb = O.bf16_narrow(c["q"])
+    c["q"] = O.bf16_widen(qb)
+    s = 1 / math.sqrt(128)
+    got = from_dev(R.flash_rows(to_dev(qb, torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                                to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                                keys=c["keys"], scale=s, table=to_dev(c["table"], torch, torch.int32),
+                                kept_pages=c["kept_pages"], page=c["page"]))
+    np.testing.assert_allclose(got, want(c, s), atol=4e-3, rtol=0)
+
+
 def test_prefill_flash_window_and_gqa():
     c = paged_case(8, [200], heads=8, kv_heads=2, pos=([0] * 200, list(range(200))))
     np.testing.assert_allclose(run("flash", c, 0.25, back=40), want(c, 0.25, "back", 40), atol=ATOL, rtol=0)
