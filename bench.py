@@ -45,6 +45,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--no-gemm", action="store_true")
     p.add_argument("--no-rows", action="store_true", help="skip the C3/C4/C5 measurements")
+    p.add_argument("--rows-only", action="store_true",
+                   help="run only the C3/C4/C5 measurements (for kernel traces of those rows)")
     p.add_argument("--roofline-only", action="store_true",
                    help="run only the lm_head lanes kernel and a plain copy of known size "
                         "(the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
@@ -300,6 +302,10 @@ def main():
         roof = lm_head_roofline(torch, reps=5)
         copy_reference(torch)
         print(json.dumps({"roofline": roof}), flush=True)
+        return
+    if a.rows_only:
+        print(json.dumps({"c3_decode": c3_decode(torch), "c3_prefill": c3_prefill(torch), "c4_fp8": c4(torch),
+                          "c5_moe": c5(torch)}), flush=True)
         return
     from tessera_amd.qwen3 import Qwen3, default_config
     cfg = default_config(max_context=PROMPT + max(a.steps, a.warmup) + 1, max_prompt=PROMPT)
