@@ -21,10 +21,14 @@
 //  * A group's waves (up to 8) split its keys and merge (max, sum, acc) in LDS.
 //    Short contexts (the batch-1 decode) take one group per (row, kv head).
 //    Long ones split keys across groups too: each writes its partial to the
-//    workspace and a second small kernel merges them in partition order. A
+//    workspace and a second small kernel merges them in partition order. Past
+//    2048 keys (no fused step) attend_long_kernel streams many key blocks per wave
+//    with the next block's loads in flight. A
 //    kernel boundary orders the two: a device-wide fence inside one kernel costs
 //    more than the merge launch.
 #include <string.h>
+
+#include <algorithm>
 
 #include "common.h"
 
@@ -347,6 +351,213 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
     TS_MARK(p.marks, 11);
 }
 
+// Long contexts (no fused step): each wave streams L iterations of 32 keys (two
+// 16-key blocks), loading iteration it + 1 while it computes iteration it; the
+// group's page-table entries are copied to LDS once; a group whose keys all lie
+// outside the row's range writes an empty partial and leaves without loading.
+// Same per-block math and partial layout as attend_rows_kernel.
+constexpr int kLongWaves = 8;
+constexpr uint32_t kLongPages = 1024;  // page-table entries a group keeps in LDS
+
+template <int G>
+struct LongBuf {
+    u32x4 kk[2][4], vq[2][4];
+};
+
+template <int G>
+__global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams p, uint32_t iters) {
+    static_assert(G * kLongWaves <= 64, "LDS budget: waves x G <= 64");
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z, parts = gridDim.x;
+    const uint32_t col = lane & 15, grp = lane >> 4;
+
+    __shared__ __attribute__((aligned(16))) float sp[kLongWaves][G][16];
+    __shared__ float sm[kLongWaves][G], sl[kLongWaves][G];
+    __shared__ __attribute__((aligned(16))) float so[kLongWaves][G][128];
+    __shared__ uint32_t stab[kLongPages];
+
+    const uint32_t pos = p.positions[r], slot = p.slots[r];
+    const uint32_t from = pos > p.back ? pos - p.back : 0;
+    const uint32_t span_keys = kLongWaves * 32 * iters;  // keys of one group
+    const uint32_t g0 = part * span_keys, g1 = g0 + span_keys;
+    const size_t gi = (size_t)r * p.kv_heads + kvh;
+    float *mine = p.partials + (gi * parts + part) * G * 130;
+    if (g0 > pos || g1 <= from) {  // nothing in range: an empty partial for the merge
+        for (uint32_t e = threadIdx.x; e < G * 130; e += blockDim.x) mine[e] = (e % 130 == 0) ? -INFINITY : 0.0f;
+        return;
+    }
+    const uint32_t pmask = (1u << p.page_shift) - 1;
+    const uint32_t p0 = g0 >> p.page_shift;
+    if (p.table) {
+        const uint32_t np = min((min(g1, pos + 1) - 1) >> p.page_shift, p.kept_pages - 1) - p0 + 1;
+        for (uint32_t i = threadIdx.x; i < np; i += blockDim.x)
+            stab[i] = p.table[(uint64_t)slot * p.kept_pages + p0 + i];
+        __syncthreads();
+    }
+    const uint32_t w0 = g0 + wave * 32 * iters;  // this wave's first key
+
+    // Block at kb (clamped into [0, pos] so its page exists): K 4 x 16B per lane (key
+    // col, d 32 grp..+32), V 4 x 16B (key 4j + grp, d 8 col..+8).
+    auto load = [&](uint32_t kb, u32x4 (&kk)[4], u32x4 (&vq)[4]) {
+        const uint32_t kbc = min(kb, pos) & ~15u;
+        const uint64_t row0 = p.table ? (((uint64_t)stab[(kbc >> p.page_shift) - p0] << p.page_shift) | (kbc & pmask))
+                                      : (uint64_t)slot * p.keys + kbc;
+        const uint32_t room = p.table ? 15u : p.keys - 1 - min(kbc, p.keys - 1);
+        const uint16_t *kr = p.k + ((row0 + min(col, room)) * p.kv_heads + kvh) * 128 + 32 * grp;
+#pragma unroll
+        for (int j = 0; j < 4; j++) kk[j] = *((const u32x4 *)kr + j);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t i = 4 * j + grp;
+            vq[j] = *(const u32x4 *)(p.v + ((row0 + min(i, room)) * p.kv_heads + kvh) * 128 + 8 * col);
+        }
+    };
+    LongBuf<G> buf[2];
+    load(w0, buf[0].kk[0], buf[0].vq[0]);
+    load(w0 + 16, buf[0].kk[1], buf[0].vq[1]);
+
+    // q operand: row (head) col of the group, d-group grp; two bf16 parts.
+    u32x4 qh[4], ql[4];
+    {
+        const bool ok = col < G;
+        const float4 *qr = (const float4 *)(p.q + ((size_t)r * p.heads + kvh * G + (ok ? col : 0)) * 128 + 32 * grp);
+        float4 qv[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) qv[i] = qr[i];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float f[8] = {qv[2 * j].x, qv[2 * j].y, qv[2 * j].z, qv[2 * j].w,
+                                qv[2 * j + 1].x, qv[2 * j + 1].y, qv[2 * j + 1].z, qv[2 * j + 1].w};
+            uint32_t h[4], l[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float a = ok ? f[2 * e] : 0.0f, b = ok ? f[2 * e + 1] : 0.0f;
+                const float ha = bf16_round(a), hb = bf16_round(b);
+                h[e] = pack_bf16x2(ha, hb);
+                l[e] = pack_bf16x2(a - ha, b - hb);
+            }
+            qh[j] = u32x4{h[0], h[1], h[2], h[3]};
+            ql[j] = u32x4{l[0], l[1], l[2], l[3]};
+        }
+    }
+
+    float m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
+    float o[G][8];
+#pragma unroll
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
+
+    // One 16-key block: scores on the matrix unit, online softmax, P*V on the VALU.
+    auto block = [&](uint32_t kb, const u32x4 (&kk)[4], const u32x4 (&vq)[4]) {
+        if (kb > pos || kb + 16 <= from) return;  // uniform across the wave
+        const uint32_t key = kb + col;
+        f32x4 sc = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            sc = mfma16(as_bf16x8(qh[j]), as_bf16x8(kk[j]), sc);
+            sc = mfma16(as_bf16x8(ql[j]), as_bf16x8(kk[j]), sc);
+        }
+        const bool valid = key >= from && key <= pos;
+        float alpha[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float si = valid ? sc[i] * p.scale : -INFINITY;
+            const float mn = fmaxf(m[i], row16_max(si));
+            alpha[i] = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
+            const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
+            l[i] = l[i] * alpha[i] + row16_sum(pi);
+            m[i] = mn;
+            const uint32_t h = 4 * grp + i;
+            if (h < G) sp[wave][h][col] = pi;
+        }
+        __builtin_amdgcn_wave_barrier();  // the wave reads back its own LDS writes
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float a = __shfl(alpha[h & 3], (h >> 2) * 16, 64);
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[h][e] *= a;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t i = 4 * j + grp, kpos = kb + i;
+            const bool ok = kpos >= from && kpos <= pos;  // p is zero outside; keep v finite too
+            const u32x4 v = vq[j];
+            const uint32_t w4[4] = {ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                const float pk = sp[wave][h][i];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    o[h][2 * e] += pk * lo_bf16(w4[e]);
+                    o[h][2 * e + 1] += pk * hi_bf16(w4[e]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+
+    // Iterations in pairs so each buffer stays in registers: load it + 1 into the
+    // other buffer, then compute it.
+    for (uint32_t it = 0; it < iters; it += 2) {
+        const uint32_t kb0 = w0 + 32 * it;
+        if (it + 1 < iters) {
+            load(kb0 + 32, buf[1].kk[0], buf[1].vq[0]);
+            load(kb0 + 48, buf[1].kk[1], buf[1].vq[1]);
+        }
+        block(kb0, buf[0].kk[0], buf[0].vq[0]);
+        block(kb0 + 16, buf[0].kk[1], buf[0].vq[1]);
+        if (it + 1 >= iters) break;
+        if (it + 2 < iters) {
+            load(kb0 + 64, buf[0].kk[0], buf[0].vq[0]);
+            load(kb0 + 80, buf[0].kk[1], buf[0].vq[1]);
+        }
+        block(kb0 + 32, buf[1].kk[0], buf[1].vq[0]);
+        block(kb0 + 48, buf[1].kk[1], buf[1].vq[1]);
+    }
+
+    // Merge the waves of this group into its partial.
+    if (col == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t h = 4 * grp + i;
+            if (h < G) { sm[wave][h] = m[i]; sl[wave][h] = l[i]; }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float v = o[h][e];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            o[h][e] = v;
+        }
+    if (grp == 0) {
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            *(float4 *)&so[wave][h][8 * col] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            *(float4 *)&so[wave][h][8 * col + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+        }
+    }
+    __syncthreads();
+    for (uint32_t e = threadIdx.x; e < G * 128; e += blockDim.x) {
+        const uint32_t h = e / 128, d = e % 128;
+        float M = -INFINITY;
+        for (uint32_t w = 0; w < kLongWaves; w++) M = fmaxf(M, sm[w][h]);
+        float L = 0.0f, O = 0.0f;
+        for (uint32_t w = 0; w < kLongWaves; w++) {
+            const float f = (sm[w][h] == -INFINITY) ? 0.0f : expf(sm[w][h] - M);
+            L += sl[w][h] * f;
+            O += so[w][h][d] * f;
+        }
+        mine[h * 130 + 2 + d] = O;
+        if (d == 0) { mine[h * 130] = M; mine[h * 130 + 1] = L; }
+    }
+}
+
 // Merges the partitions of one (row, kv head) in partition order.
 template <int G>
 __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t parts) {
@@ -370,7 +581,11 @@ __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t 
 
 struct Split {
     uint32_t wave_keys, parts, waves;  // wave_keys: 16 or 32 (one or two blocks per wave)
+    uint32_t iters;                    // > 0: the long-context kernel, iters x 32 keys per wave
 };
+
+// Spans beyond this go to attend_long_kernel (without the fused step, G <= 4).
+constexpr uint32_t kLongSpan = 2048;
 
 Split split(const ts_rows_args *a, bool step) {
     const uint32_t G = a->heads / a->kv_heads;
@@ -383,6 +598,15 @@ Split split(const ts_rows_args *a, bool step) {
     s.waves = s.parts == 1 ? (span + s.wave_keys - 1) / s.wave_keys : max_waves;
     // The fused step gives each of its G + 2 rows (q heads, new k, new v) a wave.
     if (step && s.waves < G + 2) s.waves = (G + 2) < max_waves ? G + 2 : max_waves;
+    s.iters = 0;
+    if (!step && span > kLongSpan && G <= 4) {
+        // Long contexts: each wave streams iters x 32 keys, a group 8 waves of them;
+        // about a quarter of the longest span per group keeps ~4 groups per (row, kv head).
+        s.iters = std::max(1u, std::min(32u, span / (4 * kLongWaves * 32)));
+        s.wave_keys = 32;
+        s.waves = kLongWaves;
+        s.parts = (span + kLongWaves * 32 * s.iters - 1) / (kLongWaves * 32 * s.iters);
+    }
     return s;
 }
 
@@ -451,7 +675,18 @@ int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     case 16: k = pick_nb<16, STEP>(s.wave_keys); merge = attend_rows_merge<16>; break;
     default: return ts::fail(TS_ERR_ARG, "attend_rows: %u query heads per kv head (1, 2, 4, 8 or 16)", p.G);
     }
-    hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(s.waves * 64), 0, (hipStream_t)stream, p);
+    if (!STEP && s.iters) {
+        void (*kl)(RowsParams, uint32_t) = nullptr;
+        switch (p.G) {
+        case 1: kl = attend_long_kernel<1>; break;
+        case 2: kl = attend_long_kernel<2>; break;
+        default: kl = attend_long_kernel<4>; break;
+        }
+        hipLaunchKernelGGL(kl, dim3(s.parts, a->kv_heads, a->rows), dim3(kLongWaves * 64), 0, (hipStream_t)stream, p,
+                           s.iters);
+    } else {
+        hipLaunchKernelGGL(k, dim3(s.parts, a->kv_heads, a->rows), dim3(s.waves * 64), 0, (hipStream_t)stream, p);
+    }
     TS_CHECK_LAUNCH("attend_rows launch");
     if (s.parts > 1) {
         hipLaunchKernelGGL(merge, dim3(a->kv_heads, a->rows), dim3(256), 0, (hipStream_t)stream, p, s.parts);

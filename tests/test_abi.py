@@ -65,5 +65,8 @@ def test_workspace_sizes():
     r.max_position = 150
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 0  # one group per (row, kv head)
     r.max_position = 8191
-    # 8 waves x 32 keys per group: 32 partitions of (max, sum, 128 acc) per (row, kv head, head)
-    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 32 * 2 * 130 * 4
+    # long context: 8 waves x 8 iterations x 32 keys per group, 4 partitions of
+    # (max, sum, 128 acc) per (row, kv head, head)
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 4 * 2 * 130 * 4
+    r.max_position = 2047  # the short-context kernel: 8 waves x 32 keys, 8 partitions
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 8 * 2 * 130 * 4
