@@ -7,7 +7,12 @@
 //
 // gfx950 design:
 //  * 128x128 output tile per 256-thread group (4 waves in 2x2, each 64x64 =
-//    4x4 v_mfma_f32_16x16x32_bf16 tiles), k in 64-deep steps.
+//    4x4 v_mfma_f32_16x16x32_bf16 tiles), k in 64-deep steps; 64x64 tiles (waves of
+//    32x32) when 128x128 would give fewer than 2 groups per CU, since each group is a
+//    latency chain (load, LDS, barrier, store) rather than MFMA-bound.
+//  * The MFMA computes the transposed tile (weights as the first operand), so a lane
+//    holds 4 consecutive output columns of one row: one 8-byte (bf16) or 16-byte (f32)
+//    store per 4 outputs instead of four 2- or 4-byte ones.
 //  * Both operands are k-contiguous ([m,k] and [n,k]), which is the matrix
 //    unit's native operand order: a lane's 8 k values are one 16-byte LDS read.
 //  * LDS holds two stages (A and B, 16 KiB each per stage, plus a second A
@@ -25,7 +30,7 @@
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int BM = 128, BN = 128, BK = 64;  // the default tile; BT = 64 for products with few tiles
 constexpr int kThreads = 256;
 
 struct TiledParams {
@@ -45,24 +50,27 @@ struct TiledParams {
     uint32_t matrices, repeat, stride, offset;
 };
 
-// Byte offset of (row, chunk) in a swizzled [128 rows][8 chunks of 16B] tile.
+// Byte offset of (row, chunk) in a swizzled [rows][8 chunks of 16B] tile.
 TS_DEV uint32_t swz(uint32_t row, uint32_t chunk) { return row * 128 + ((chunk ^ (row & 7)) << 4); }
 
-template <bool XF32, bool W8, bool SILU>
+template <int BT, bool XF32, bool W8, bool SILU>
 struct Loader {
-    // Per thread per stage: A: 4 chunks (rows t/8 + 32i, chunk t%8), B: 4 chunks.
-    u32x4 a_hi[4], a_lo[4], b[4];
-    // x row of each of this thread's 4 A rows, or -1 for a zero row.
-    int64_t src[4];
+    static constexpr int RPT = BT / 32;  // rows per thread per operand
+    static constexpr int WT = BT / 2;    // a wave's share of the tile's columns
+    // Per thread per stage: A: RPT chunks (rows t/8 + 32i, chunk t%8), B: RPT chunks.
+    u32x4 a_hi[RPT], a_lo[RPT], b[RPT];
+    // x row of each of this thread's A rows, or -1 for a zero row.
+    int64_t src[RPT];
     // The weights of this tile's matrix (the whole w outside picked products).
     const void *w;
     const uint16_t *w_scale;
 
-    // Weight row of B-tile row `br` for this output tile.
+    // Weight row of B-tile row `br` for this output tile. SILU: each wave's WT rows are
+    // WT/2 gate rows then the WT/2 up rows of the same output columns.
     TS_DEV static uint32_t wrow(uint32_t br, uint32_t n0, uint32_t N) {
         if (!SILU) return n0 + br;
-        const uint32_t half = br >> 6, within = br & 63;
-        return within < 32 ? n0 + half * 32 + within : N + n0 + half * 32 + (within - 32);
+        const uint32_t half = br / WT, within = br % WT;
+        return within < WT / 2 ? n0 + half * (WT / 2) + within : N + n0 + half * (WT / 2) + (within - WT / 2);
     }
 
     TS_DEV void fetch(const TiledParams &p, uint32_t m0, uint32_t n0, uint32_t k0) {
@@ -70,7 +78,7 @@ struct Loader {
         const uint32_t kk = k0 + chunk * 8;
         const bool kin = kk < p.k;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < RPT; i++) {
             const uint32_t r = (t >> 3) + 32 * i;
             const bool ain = src[i] >= 0 && kin;
             if (XF32) {
@@ -99,7 +107,7 @@ struct Loader {
             }
             const uint32_t nr = wrow(r, n0, p.n);
             const uint32_t nrows = SILU ? 2 * p.n : p.n;
-            const bool nin = (SILU ? (n0 + (r >> 6) * 32 + (r & 31)) < p.n : nr < nrows) && kin;
+            const bool nin = (SILU ? (n0 + (r / WT) * (WT / 2) + (r % (WT / 2))) < p.n : nr < nrows) && kin;
             if (W8) {
                 if (nin) {
                     const u32x2 c = *(const u32x2 *)((const uint8_t *)w + (size_t)nr * p.k + kk);
@@ -117,7 +125,7 @@ struct Loader {
     TS_DEV void store(char *sa, char *sa_lo, char *sb) {
         const uint32_t t = threadIdx.x, chunk = t & 7;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < RPT; i++) {
             const uint32_t r = (t >> 3) + 32 * i;
             *(u32x4 *)(sa + swz(r, chunk)) = a_hi[i];
             if (XF32) *(u32x4 *)(sa_lo + swz(r, chunk)) = a_lo[i];
@@ -126,19 +134,21 @@ struct Loader {
     }
 };
 
-template <bool XF32, bool W8, bool SILU, bool PICK>
+template <int BT, bool XF32, bool W8, bool SILU, bool PICK>
 __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
-    constexpr int TILE = BM * BK * 2;  // bytes of one operand stage
+    constexpr int TILE = BT * BK * 2;         // bytes of one operand stage
+    constexpr int WT = BT / 2, FT = WT / 16;  // wave tile, 16x16 fragments per wave side
+    constexpr int RPT = BT / 32;
     __shared__ __attribute__((aligned(16))) char lds[2][XF32 ? 3 : 2][TILE];
-    __shared__ uint32_t rows_out[PICK ? BM : 1];  // output row of each tile row (PICK)
+    __shared__ uint32_t rows_out[PICK ? BT : 1];  // output row of each tile row (PICK)
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t wm = wave >> 1, wn = wave & 1;
     const uint32_t col = lane & 15, grp = lane >> 4;
-    const uint32_t n0 = blockIdx.x * (SILU ? BN / 2 : BN);  // SILU: 64 output columns per tile
+    const uint32_t n0 = blockIdx.x * (SILU ? BT / 2 : BT);  // SILU: BT / 2 output columns per tile
 
-    Loader<XF32, W8, SILU> ld;
-    uint32_t m0 = blockIdx.y * BM, mend = p.m;  // tile rows [m0, min(m0 + BM, mend))
+    Loader<BT, XF32, W8, SILU> ld;
+    uint32_t m0 = blockIdx.y * BT, mend = p.m;  // tile rows [m0, min(m0 + BT, mend))
     ld.w = p.w;
     ld.w_scale = p.w_scale;
     if (PICK) {
@@ -152,27 +162,27 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
             else hi = mid;
         }
         const uint32_t e = lo;
-        m0 = p.row_start[e] + (y - p.tile_start[e]) * BM;
+        m0 = p.row_start[e] + (y - p.tile_start[e]) * BT;
         mend = p.row_start[e + 1];
         const size_t first_row = (size_t)e * p.stride + p.offset;
         ld.w = (const char *)p.w + first_row * p.k * (W8 ? 1 : 2);
         if (W8) ld.w_scale = p.w_scale + first_row;
-        for (uint32_t r = threadIdx.x; r < BM; r += kThreads)
+        for (uint32_t r = threadIdx.x; r < BT; r += kThreads)
             rows_out[r] = m0 + r < mend ? p.perm[m0 + r] : 0xffffffffu;
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < RPT; i++) {
         const uint32_t r = (threadIdx.x >> 3) + 32 * i;
         if (PICK) ld.src[i] = rows_out[r] != 0xffffffffu ? (int64_t)(rows_out[r] / p.repeat) : -1;
         else ld.src[i] = m0 + r < p.m ? (int64_t)(m0 + r) : -1;
     }
 
-    f32x4 acc[4][4];
+    f32x4 acc[FT][FT];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < FT; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f32x4{0, 0, 0, 0};
+        for (int j = 0; j < FT; j++) acc[i][j] = f32x4{0, 0, 0, 0};
 
     const uint32_t steps = (p.k + BK - 1) / BK;
     ld.fetch(p, m0, n0, 0);
@@ -186,21 +196,21 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             const uint32_t chunk = ks * 4 + grp;
-            bf16x8 af[4], al[4], bfr[4];
+            bf16x8 af[FT], al[FT], bfr[FT];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t ra = wm * 64 + i * 16 + col;
+            for (int i = 0; i < FT; i++) {
+                const uint32_t ra = wm * WT + i * 16 + col;
                 af[i] = as_bf16x8(*(const u32x4 *)(sa + swz(ra, chunk)));
                 if (XF32) al[i] = as_bf16x8(*(const u32x4 *)(sl + swz(ra, chunk)));
-                const uint32_t rb = wn * 64 + i * 16 + col;
+                const uint32_t rb = wn * WT + i * 16 + col;
                 bfr[i] = as_bf16x8(*(const u32x4 *)(sb + swz(rb, chunk)));
             }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < FT; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
-                    if (XF32) acc[i][j] = mfma16(al[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < FT; j++) {
+                    acc[i][j] = mfma16(bfr[j], af[i], acc[i][j]);
+                    if (XF32) acc[i][j] = mfma16(bfr[j], al[i], acc[i][j]);
                 }
         }
         if (s + 1 < steps) {
@@ -210,41 +220,53 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
         __syncthreads();
     }
 
-    // Epilogue. D lane layout: column col, rows 4*grp + r of each 16x16 tile.
+    // Epilogue. acc[i][j] is the transposed 16x16 tile: lane (col, grp) holds row
+    // m = wm WT + 16 i + col and columns n = wn WT + 16 j + 4 grp + 0..3 (SILU: gate in
+    // j < FT/2, up in j + FT/2, columns wn WT/2 + 16 j + 4 grp + 0..3).
     const uint32_t N = p.n;
     const uint16_t *scale = ld.w_scale;
+    const bool vec = (N & 3) == 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < FT; i++) {
+        const uint32_t tr = wm * WT + i * 16 + col;
+        if (m0 + tr >= mend) continue;
+        const uint32_t m = PICK ? rows_out[tr] : m0 + tr;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t tr = wm * 64 + i * 16 + 4 * grp + r;
-            if (m0 + tr >= mend) continue;
-            const uint32_t m = PICK ? rows_out[tr] : m0 + tr;
-            if (!SILU) {
+        for (int j = 0; j < (SILU ? FT / 2 : FT); j++) {
+            const uint32_t n = n0 + (SILU ? wn * (WT / 2) : wn * WT) + j * 16 + 4 * grp;
+            if (n >= N) continue;
+            float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t n = n0 + wn * 64 + j * 16 + col;
-                    if (n >= N) continue;
-                    float v = acc[i][j][r];
-                    if (W8) v *= bf16_float(scale[n]);
-                    if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
-                    if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
-                    else ((float *)p.out)[(size_t)m * N + n] = v;
+            for (int r = 0; r < 4; r++) {
+                float g = acc[i][j][r];
+                if (SILU) {
+                    float u = acc[i][j + FT / 2][r];
+                    if (W8) {
+                        g *= bf16_float(scale[min(n + r, N - 1)]);
+                        u *= bf16_float(scale[N + min(n + r, N - 1)]);
+                    }
+                    v[r] = g / (1.0f + expf(-g)) * u;
+                } else {
+                    if (W8) g *= bf16_float(scale[min(n + r, N - 1)]);
+                    v[r] = g;
                 }
+            }
+            const size_t at = (size_t)m * N + n;
+            if (vec && n + 3 < N) {
+                if (p.stages & TS_AFTER_ADD) {
+                    const float4 a = *(const float4 *)(p.a0 + at);
+                    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+                }
+                if (p.out_bf16) *(u32x2 *)((uint16_t *)p.out + at) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                else *(float4 *)((float *)p.out + at) = float4{v[0], v[1], v[2], v[3]};
             } else {
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const uint32_t n = n0 + wn * 32 + j * 16 + col;
-                    if (n >= N) continue;
-                    float g = acc[i][j][r], u = acc[i][j + 2][r];
-                    if (W8) {
-                        g *= bf16_float(scale[n]);
-                        u *= bf16_float(scale[N + n]);
-                    }
-                    float v = g / (1.0f + expf(-g)) * u;
-                    if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
-                    if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
-                    else ((float *)p.out)[(size_t)m * N + n] = v;
+                for (int r = 0; r < 4; r++) {
+                    if (n + r >= N) break;
+                    float u = v[r];
+                    if (p.stages & TS_AFTER_ADD) u += p.a0[at + r];
+                    if (p.out_bf16) ((uint16_t *)p.out)[at + r] = bf16_bits(u);
+                    else ((float *)p.out)[at + r] = u;
                 }
             }
         }
@@ -253,15 +275,15 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
 
 using Kern = void (*)(TiledParams);
 
-template <bool XF32, bool W8, bool PICK>
+template <int BT, bool XF32, bool W8, bool PICK>
 Kern pick_silu(bool silu) {
-    return silu ? tiled_kernel<XF32, W8, true, PICK> : tiled_kernel<XF32, W8, false, PICK>;
+    return silu ? tiled_kernel<BT, XF32, W8, true, PICK> : tiled_kernel<BT, XF32, W8, false, PICK>;
 }
 
-template <bool PICK>
+template <int BT, bool PICK>
 Kern pick_kernel(bool xf, bool w8, bool silu) {
-    return xf ? (w8 ? pick_silu<true, true, PICK>(silu) : pick_silu<true, false, PICK>(silu))
-              : (w8 ? pick_silu<false, true, PICK>(silu) : pick_silu<false, false, PICK>(silu));
+    return xf ? (w8 ? pick_silu<BT, true, true, PICK>(silu) : pick_silu<BT, true, false, PICK>(silu))
+              : (w8 ? pick_silu<BT, false, true, PICK>(silu) : pick_silu<BT, false, false, PICK>(silu));
 }
 
 }  // namespace
@@ -285,12 +307,18 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TiledParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
-    const uint32_t cols = silu ? BN / 2 : BN;
-    const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->m + BM - 1) / BM;
+    // 64x64 tiles when 128x128 would give fewer than 2 groups per CU: more groups to
+    // hide each one's load/store latency chain (measured: MFMA time is not the limit).
+    const uint64_t big_tiles = (uint64_t)((a->n + (silu ? BN / 2 : BN) - 1) / (silu ? BN / 2 : BN)) *
+                               ((a->m + BM - 1) / BM);
+    const int bt = big_tiles < 512 ? 64 : 128;
+    const uint32_t cols = silu ? bt / 2 : bt;
+    const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->m + bt - 1) / bt;
     TS_REQUIRE(gy <= 65535, "tiled: m=%u too large for one launch", a->m);
     p.perm = p.row_start = p.tile_start = nullptr;
     p.matrices = 0; p.repeat = 1; p.stride = 0; p.offset = 0;
-    Kern k = pick_kernel<false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
+    Kern k = bt == 64 ? pick_kernel<64, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu)
+                      : pick_kernel<128, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("tiled launch");
     return TS_OK;
@@ -343,7 +371,7 @@ extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
     const uint32_t cols = silu ? BN / 2 : BN;
     // Row tiles: at most one partial tile per matrix beyond rows / BM full ones.
     const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->rows + BM - 1) / BM + a->count;
-    Kern k = pick_kernel<true>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
+    Kern k = pick_kernel<BM, true>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("picked launch");
     return TS_OK;

@@ -91,7 +91,7 @@ def test_lanes_and_tiled_agree_at_16_rows():
     _check(a, b, _bound(x, wf))
 
 
-@pytest.mark.parametrize("m", [1, 5, 40])
+@pytest.mark.parametrize("m", [1, 5, 40, 100, 300])
 def test_fused_stages(m):
     """RmsNorm before (lanes only), SiLU*up and the residual add after."""
     R = _rules()
@@ -176,3 +176,20 @@ def test_e4m3_decode_every_code(m):
         nan = np.isnan(want)
         assert np.array_equal(np.isnan(row), nan)
         assert np.array_equal(row[~nan], want[~nan].astype(np.float32))
+
+
+def test_silu_pair_big_tiles():
+    """SiLU pair + residual on the 128x128 tiled kernel (enough tiles: 2048 x 4096)."""
+    R = _rules()
+    O.set_threads(O.lib().or_threads_available())
+    r = rng(21)
+    m, k, n = 2048, 64, 4096
+    x = r.standard_normal((m, k)).astype(np.float32)
+    wb, wf = bf16_bits_normal(r, (2 * n, k), 0.05)
+    res = r.standard_normal((m, n)).astype(np.float32)
+    gu = O.product_bf16w(x, wb)
+    O.set_threads(1)
+    want = O.act("silu", gu[:, :n]) * gu[:, n:] + res
+    got = from_dev(R.linear(to_dev(x, torch), to_dev(wb, torch), silu_mul=True, a0=to_dev(res, torch)))
+    b = _bound(x, wf)
+    _check(got, want, 1.1 * b[:, :n] * np.abs(gu[:, n:]) + np.abs(gu[:, :n]) * b[:, n:] + 1e-5)
