@@ -63,23 +63,23 @@ int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n
 // mantissa bits; the bit form below gives the same code for every f32,
 // subnormals and overflow to infinity included).
 // ---------------------------------------------------------------------------
-TS_DEV uint16_t bf16_bits(float x) {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)(((u >> 16) & 0x8000u) | 0x7fc0u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+// f32 -> bf16, round to nearest even, on gfx950's conversion instruction
+// (v_cvt_pk_bf16_f32); NaN becomes sign | 0x7fc0 through a select, not a branch (a
+// branch per value made the exec-mask bookkeeping cost more than the work).
+typedef __bf16 ts_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ts_f32x2 __attribute__((ext_vector_type(2)));
+TS_DEV uint32_t pack_bf16x2(float a, float b) {
+    uint32_t r = __builtin_bit_cast(uint32_t, __builtin_convertvector(ts_f32x2{a, b}, ts_bf16x2));
+    const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+    const uint32_t na = ((ua >> 16) & 0x8000u) | 0x7fc0u, nb = (ub & 0x80000000u) | 0x7fc00000u;
+    r = (ua & 0x7fffffffu) > 0x7f800000u ? (r & 0xffff0000u) | na : r;
+    r = (ub & 0x7fffffffu) > 0x7f800000u ? (r & 0x0000ffffu) | nb : r;
+    return r;
 }
-
+TS_DEV uint16_t bf16_bits(float x) { return (uint16_t)(pack_bf16x2(x, 0.0f) & 0xffffu); }
 TS_DEV float bf16_float(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
 TS_DEV float bf16_round(float x) { return bf16_float(bf16_bits(x)); }
 
-// Two f32 -> packed bf16 pair in one u32 (low half first).
-TS_DEV uint32_t pack_bf16x2(float a, float b) {
-    return (uint32_t)bf16_bits(a) | ((uint32_t)bf16_bits(b) << 16);
-}
-
-// Low / high bf16 of a packed u32, as f32 (exact).
 TS_DEV float lo_bf16(uint32_t v) { return __uint_as_float(v << 16); }
 TS_DEV float hi_bf16(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 

@@ -193,3 +193,37 @@ def test_silu_pair_big_tiles():
     got = from_dev(R.linear(to_dev(x, torch), to_dev(wb, torch), silu_mul=True, a0=to_dev(res, torch)))
     b = _bound(x, wf)
     _check(got, want, 1.1 * b[:, :n] * np.abs(gu[:, n:]) + np.abs(gu[:, :n]) * b[:, n:] + 1e-5)
+
+
+def test_bf16_output_rounding_matches_oracle():
+    """The device's f32 -> bf16 rounding (every bf16 store) is the reference's RNE
+    (scalar.rs): out = x * 1.0 through a 4-row product with bf16 output, over random
+    values of every exponent, exact ties, denormals, values next to overflow, +-inf,
+    NaN and +-0; bit-exact (NaN compared as NaN; -0 becomes +0 because the product's
+    sum starts at +0, as the reference's Acc does)."""
+    R = _rules()
+    r = rng(123)
+    bits = r.integers(0, 2 ** 32, 4000, dtype=np.uint64).astype(np.uint32)
+    ties = (r.integers(0, 2 ** 16, 200, dtype=np.uint64).astype(np.uint32) << 16) | 0x8000
+    special = np.array([0x00000001, 0x00008000, 0x0000ffff, 0x007fffff, 0x00800000, 0x7f7f8000, 0x7f7fffff,
+                        0x7f800000, 0xff800000, 0x7fc00001, 0xffa00000, 0x80000000, 0x00000000, 0x3f808000,
+                        0x3f818000], np.uint32)
+    vals = np.concatenate([bits, ties, special]).view(np.float32)
+    vals = np.concatenate([vals, np.zeros((-len(vals)) % 4, np.float32)])
+    w = np.zeros((1, 8), np.uint16)
+    w[0, 0] = O.bf16_narrow(np.array([1.0], np.float32))[0]
+    wd = to_dev(w, torch)
+    got = []
+    for i in range(0, len(vals), 4):
+        x = np.zeros((4, 8), np.float32)
+        x[:, 0] = vals[i:i + 4]
+        out = R.linear(to_dev(x, torch), wd, out_dtype=torch.bfloat16)
+        got.append(out.view(torch.int16).cpu().numpy().view(np.uint16)[:, 0])
+    got = np.concatenate(got)
+    want = O.bf16_narrow(vals)
+    want[vals == 0] = 0  # +0 + (-0 * 1) = +0
+    nan = np.isnan(vals)
+    bad = np.nonzero((got != want) & ~nan)[0]
+    assert bad.size == 0, "x bits / got / want: " + ", ".join(
+        f"{vals[i:i + 1].view(np.uint32)[0]:08x}/{got[i]:04x}/{want[i]:04x}" for i in bad[:12]) + f" ({bad.size} differ)"
+    assert np.all((got[nan] & 0x7fff) > 0x7f80)
