@@ -68,6 +68,22 @@ int tessera_qwen3_logits(ts_qwen3 *m, float *host, uint64_t count);
 /* 1: capture the decode step into a HIP graph (default); 0: eager launches. */
 int tessera_qwen3_set_graph(ts_qwen3 *m, int on);
 
+/* 1: run decode steps as one persistent launch per decode call (every layer, the
+ * lm_head and the greedy pick of all `steps` tokens in one grid of one group per
+ * CU; the default when the shape fits: head_dim 128, two q heads per kv head,
+ * hidden <= 1024, ffn <= 3072, at most 32 layers); 0: the graph of kernels (or
+ * eager launches, see tessera_qwen3_set_graph). Returns an error for 1 when the
+ * shape does not fit. No counterpart in the reference, whose decode step is a
+ * graph of its lowered kernels (engine/plan/run/src/device.rs:227-245). */
+int tessera_qwen3_set_step(ts_qwen3 *m, int on);
+/* 1 when decode runs the persistent step. */
+int tessera_qwen3_step_mode(ts_qwen3 *m);
+
+/* Debug: the persistent step writes phase stamps (100 MHz clock) of the first
+ * step of each later launch to `marks` (device memory of groups * (layers + 2)
+ * * 10 words; NULL stops it); *groups receives the grid size. */
+int tessera_qwen3_step_marks(ts_qwen3 *m, uint64_t *marks, uint32_t *groups);
+
 /* The runner's stream (a hipStream_t). */
 void *tessera_qwen3_stream(ts_qwen3 *m);
 

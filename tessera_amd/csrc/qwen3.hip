@@ -22,6 +22,7 @@
 #include "../../include/tessera_kv.h"
 #include "../../include/tessera_run.h"
 #include "common.h"
+#include "decode_step.h"
 
 #include <algorithm>
 
@@ -94,6 +95,13 @@ struct ts_qwen3 {
     bool use_graph = true;
     hipGraphExec_t graph = nullptr;
     uint32_t position = 0;
+    // The persistent step (decode_step.hip): hand-off words, error word, epoch.
+    bool step_ok = false;   // the shape fits the persistent kernel
+    bool use_step = false;  // decode runs it (default when it fits)
+    uint64_t *hand = nullptr;
+    uint32_t *d_error = nullptr;
+    uint32_t epoch = 1, groups = 0;
+    uint64_t *step_marks = nullptr;  // debug: phase stamps of the next persistent launch
 
     template <class T>
     int alloc(T **p, size_t count) {
@@ -220,6 +228,29 @@ int decode_step(ts_qwen3 *m) {
     return TS_OK;
 }
 
+// `steps` decode steps in one persistent launch (decode_step.hip).
+int launch_step(ts_qwen3 *m, uint32_t steps) {
+    const ts_qwen3_config &c = m->c;
+    ts::DecodeStepArgs a;
+    memset(&a, 0, sizeof a);
+    for (uint32_t l = 0; l < c.layers; l++) {
+        const Layer &L = m->layers[l];
+        a.qkv[l] = L.qkv; a.o[l] = L.o; a.gate_up[l] = L.gate_up; a.down[l] = L.down;
+        a.ln1[l] = L.ln1; a.ln2[l] = L.ln2; a.q_norm[l] = L.q_norm; a.k_norm[l] = L.k_norm;
+        a.k_cache[l] = L.k_cache; a.v_cache[l] = L.v_cache;
+    }
+    a.embed = m->embed; a.norm = m->norm; a.rope = m->rope; a.table = m->d_table;
+    a.tok = m->d_tok; a.pos = m->d_pos; a.hist = m->d_hist; a.logits = m->logits;
+    a.hand = m->hand; a.error = m->d_error; a.marks = m->step_marks;
+    a.H = c.hidden; a.L = c.layers; a.Hq = c.heads; a.Hkv = c.kv_heads; a.F = c.ffn; a.V = c.vocab;
+    a.NG = m->groups; a.kept_pages = m->kept_pages; a.page_shift = (uint32_t)__builtin_ctz(c.page);
+    a.steps = steps; a.epoch = m->epoch;
+    a.eps = c.eps; a.scale = 1.0f / sqrtf((float)c.head_dim);
+    TRY(ts::decode_step_launch(&a, m->stream));
+    m->epoch += steps;
+    return TS_OK;
+}
+
 size_t workspace_need(ts_qwen3 *m) {
     const ts_qwen3_config &c = m->c;
     size_t need = tessera_hip_argmax_workspace(1, c.vocab);
@@ -330,6 +361,18 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) return fail(ts::hip_status(e, "open upload"));
     m->pool = tessera_kv_new(m->total_pages, c.page);
+    rc = ts::decode_step_supported(H, c.layers, c.heads, c.kv_heads, D, c.ffn, m->kept_pages);
+    if (rc < 0) return fail(rc);
+    if (rc == TS_OK) {
+        if ((rc = ts::decode_step_groups(&m->groups))) return fail(rc);
+        const size_t words = ts::decode_step_hand_words(H, c.layers, c.heads, c.kv_heads, c.ffn, m->groups);
+        if ((rc = m->alloc(&m->hand, words)) || (rc = m->alloc(&m->d_error, 1))) return fail(rc);
+        e = hipMemsetAsync(m->hand, 0, words * 8, m->stream);
+        if (e == hipSuccess) e = hipMemsetAsync(m->d_error, 0, 4, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) return fail(ts::hip_status(e, "open: hand-off words"));
+        m->step_ok = m->use_step = true;
+    }
     *out = m;
     return TS_OK;
 }
@@ -417,7 +460,9 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
                "qwen3_decode: %u steps from position %u pass the kept context %u", steps, m->position,
                m->c.max_context);
     hipError_t e;
-    if (m->use_graph && !m->graph && steps > 0) {
+    if (m->use_step && steps > 0) {
+        TRY(launch_step(m, steps));
+    } else if (m->use_graph && !m->graph && steps > 0) {
         hipGraph_t g = nullptr;
         e = hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal);
         if (e != hipSuccess) return ts::hip_status(e, "hipStreamBeginCapture");
@@ -432,7 +477,7 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
         hipGraphDestroy(g);
         if (e != hipSuccess) return ts::hip_status(e, "hipGraphInstantiate");
     }
-    for (uint32_t i = 0; i < steps; i++) {
+    for (uint32_t i = 0; i < steps && !m->use_step; i++) {
         if (m->use_graph) {
             e = hipGraphLaunch(m->graph, m->stream);
             if (e != hipSuccess) return ts::hip_status(e, "hipGraphLaunch");
@@ -448,6 +493,16 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
     }
     e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) return ts::hip_status(e, "decode");
+    if (m->use_step && steps > 0) {
+        uint32_t err = 0;
+        e = hipMemcpy(&err, m->d_error, 4, hipMemcpyDeviceToHost);
+        if (e != hipSuccess) return ts::hip_status(e, "decode: error word");
+        if (err) {
+            // The grid left early: the step is not trusted again in this runner.
+            m->use_step = m->step_ok = false;
+            return ts::fail(TS_ERR_ARG, "qwen3_decode: a hand-off wait of the persistent step timed out");
+        }
+    }
     return TS_OK;
 }
 
@@ -462,6 +517,24 @@ extern "C" int tessera_qwen3_logits(ts_qwen3 *m, float *host, uint64_t count) {
 extern "C" int tessera_qwen3_set_graph(ts_qwen3 *m, int on) {
     TS_REQUIRE(m, "qwen3_set_graph: null");
     m->use_graph = on != 0;
+    return TS_OK;
+}
+
+extern "C" int tessera_qwen3_set_step(ts_qwen3 *m, int on) {
+    TS_REQUIRE(m, "qwen3_set_step: null");
+    TS_REQUIRE(!on || m->step_ok, "qwen3_set_step: this shape does not fit the persistent step");
+    m->use_step = on != 0;
+    return TS_OK;
+}
+
+extern "C" int tessera_qwen3_step_mode(ts_qwen3 *m) { return m && m->use_step ? 1 : 0; }
+
+// Debug: the persistent step records phase stamps into `marks` (device memory,
+// groups * (layers + 2) * 10 words) on its next launches; NULL stops it.
+extern "C" int tessera_qwen3_step_marks(ts_qwen3 *m, uint64_t *marks, uint32_t *groups) {
+    TS_REQUIRE(m && groups, "qwen3_step_marks: null");
+    m->step_marks = marks;
+    *groups = m->groups;
     return TS_OK;
 }
 

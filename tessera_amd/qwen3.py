@@ -31,6 +31,8 @@ SIGNATURES = {
     "tessera_qwen3_decode": (C.c_int, [_P, C.c_uint32, _P]),
     "tessera_qwen3_logits": (C.c_int, [_P, _P, C.c_uint64]),
     "tessera_qwen3_set_graph": (C.c_int, [_P, C.c_int]),
+    "tessera_qwen3_set_step": (C.c_int, [_P, C.c_int]),
+    "tessera_qwen3_step_mode": (C.c_int, [_P]),
     "tessera_qwen3_stream": (_P, [_P]),
     "tessera_qwen3_position": (C.c_uint32, [_P]),
     "tessera_qwen3_pages": (C.c_int, [_P, _P, C.c_uint32]),
@@ -109,6 +111,14 @@ class Qwen3:
 
     def set_graph(self, on: bool):
         abi.check(self.L.tessera_qwen3_set_graph(self.h, 1 if on else 0), "tessera_qwen3_set_graph")
+
+    def set_step(self, on: bool):
+        """True: decode as one persistent launch per call; False: the graph of kernels."""
+        abi.check(self.L.tessera_qwen3_set_step(self.h, 1 if on else 0), "tessera_qwen3_set_step")
+
+    @property
+    def step_mode(self) -> bool:
+        return bool(self.L.tessera_qwen3_step_mode(self.h))
 
     @property
     def position(self) -> int:

@@ -22,11 +22,13 @@ def small_config():
                           max_prompt=64)
 
 
-def run_case(cfg, seed, prompt, steps, cos_min, rel_max, graph=True):
+def run_case(cfg, seed, prompt, steps, cos_min, rel_max, graph=True, step=True):
     from tessera_amd.qwen3 import Qwen3
     O.set_threads(O.lib().or_threads_available())
     m = Qwen3(cfg, seed=seed)
     m.set_graph(graph)
+    m.set_step(step)
+    assert m.step_mode == step
     ref = OracleQwen3(host_weights(m))
     first = m.prefill(prompt)
     got = m.logits()
@@ -48,12 +50,35 @@ def run_case(cfg, seed, prompt, steps, cos_min, rel_max, graph=True):
     return tokens
 
 
+@pytest.mark.parametrize("step", [True, False], ids=["persistent", "graph"])
 @pytest.mark.parametrize("prompt_len", [1, 9, 40])
-def test_small_decoder_matches_oracle(prompt_len):
-    """Short prompts take the fused few-row path; 40 rows take tiled + flash."""
+def test_small_decoder_matches_oracle(prompt_len, step):
+    """Short prompts take the fused few-row path; 40 rows take tiled + flash. Decode
+    runs as the persistent step or as the graph of kernels."""
     r = np.random.default_rng(prompt_len)
     prompt = r.integers(0, 1000, prompt_len).astype(np.uint32)
-    run_case(small_config(), 7, prompt, 12, 0.99999, 1e-3)
+    run_case(small_config(), 7, prompt, 12, 0.99999, 1e-3, step=step)
+
+
+def test_persistent_steps_in_one_launch():
+    """30 steps in one persistent launch give the tokens of 30 one-step launches and
+    of the graph of kernels, and the final logits agree to f32 summation order."""
+    from tessera_amd.qwen3 import Qwen3
+    prompt = np.arange(20, dtype=np.uint32) * 37 % 1000
+    outs = []
+    for step, per_call in ((True, 30), (True, 1), (False, 1)):
+        m = Qwen3(small_config(), seed=3)
+        m.set_step(step)
+        m.prefill(prompt)
+        toks = np.concatenate([m.decode(per_call) for _ in range(30 // per_call)])
+        outs.append((toks, m.logits(), m.position))
+        m.close()
+    for toks, logits, pos in outs[1:]:
+        assert np.array_equal(outs[0][0], toks)
+        assert pos == outs[0][2] == 50
+        assert max_rel(outs[0][1], logits) <= 1e-5
+    # one launch or thirty: same arithmetic, bit for bit
+    assert np.array_equal(outs[0][1], outs[1][1])
 
 
 def test_graph_replay_equals_eager():
@@ -62,6 +87,7 @@ def test_graph_replay_equals_eager():
     outs = []
     for graph in (False, True):
         m = Qwen3(small_config(), seed=3)
+        m.set_step(False)
         m.set_graph(graph)
         m.prefill(prompt)
         toks = m.decode(30)
