@@ -33,6 +33,7 @@ SIGNATURES = {
     "tessera_qwen3_set_graph": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_set_step": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_step_mode": (C.c_int, [_P]),
+    "tessera_qwen3_step_marks": (C.c_int, [_P, _P, C.POINTER(C.c_uint32)]),
     "tessera_qwen3_stream": (_P, [_P]),
     "tessera_qwen3_position": (C.c_uint32, [_P]),
     "tessera_qwen3_pages": (C.c_int, [_P, _P, C.c_uint32]),
