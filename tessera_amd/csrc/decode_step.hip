@@ -53,6 +53,7 @@ constexpr uint32_t kCT = kCW * 64;             // compute threads
 constexpr uint32_t kThreads = (kCW + kDW) * 64;
 constexpr uint32_t kRing = 128;                // ring units of 1 KiB
 constexpr uint32_t kMaxOut = 56;               // DMA loads in flight per wave (vmcnt holds 63)
+constexpr uint32_t kBurst = 8;                 // DMA loads a wave issues per barrier
 constexpr uint32_t kRW = 4;                    // product rows per compute wave
 constexpr uint32_t kChunk = kRW * kCW;         // lm_head rows per chunk
 constexpr uint32_t kMaxXa = 3072;              // staged input floats (H, Hq*128 and F)
@@ -60,7 +61,7 @@ constexpr uint32_t kMaxH = 1024;
 constexpr uint32_t kMaxPages = 512;
 constexpr uint64_t kTimeout = 200000000ull;    // 2 s of the 100 MHz clock
 constexpr int kNX = (kMaxXa + kCT - 1) / kCT;  // staged words per compute thread
-constexpr int kPre = 3;                        // key blocks per wave loaded before q arrives
+constexpr int kPre = 7;                        // 4-key blocks per wave loaded before q arrives
 static_assert(kCW >= 4 && kCW <= 8, "attention uses waves 0..3 and LDS partials for up to 8 waves");
 
 // LDS layout (bytes).
@@ -323,52 +324,91 @@ TS_DEV void norm_rope(float &a, float &b, float ga, float gb, float cs, float sn
     b = rb;
 }
 
+// Optional phase stamps of the first step (thread 0 of every group): slot 2 ph
+// when the phase's input is staged, 2 ph + 1 when its outputs are stored, 8 when
+// the group's attention is done; row L: lm_head input, chunks done, token.
+TS_DEV void mark(const DecodeStepArgs &p, const Ctx &c, uint32_t g, uint32_t t, uint32_t l, uint32_t k) {
+    if (p.marks && t == 0 && c.tid == 0) p.marks[((size_t)g * (p.L + 2) + l) * 10 + k] = now();
+}
+
 constexpr uint32_t kAttBars = 4;  // barriers of attention()
+
+// Sums (maxima) over the four 16-lane rows of a wave, in every lane: lanes j, j + 16,
+// j + 32 and j + 48 end with the same total (gfx950 permlane swaps: VALU, no LDS).
+TS_DEV float rows4_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+TS_DEV float rows4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 
 // Attention of kv head `a` (its two q heads) at position pos over kept rows
 // [0, pos] (engine/ir/interp/src/cpu.rs:141-167, 293-351): the raw q/k/v rows
 // come from the qkv hand-off; q and the new k are normalized and rotated, the new
 // k and v rows are appended (bf16), and the two heads' outputs are published.
-// Lanes: key = lane / 8 of an 8-key block, dims 16 (lane % 8) .. +16.
+// Lanes: key = lane / 16 of a 4-key block, dims 8 (lane % 16) .. +8; a wave takes
+// blocks wave + kCW i, kPre of them per softmax pass (one max and one sum per pass,
+// then the running (max, sum, acc) rescaled once per pass).
 TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, Ctx &c, uint32_t l, uint32_t a,
                       uint32_t pos, uint32_t tag) {
     const uint32_t lane = c.lane, wave = c.wave;
-    const uint32_t kj = lane >> 3, part = lane & 7;
+#define AMARK(k) do { if (l == 5 && tag == p.epoch) mark(p, c, a, 0, p.L + 1, k); } while (0)
+    AMARK(0);
+    const uint32_t kr = lane >> 4, part = lane & 15;
     const uint32_t Hkv = p.Hkv, shift = p.page_shift, mask = (1u << shift) - 1;
     const uint16_t *kc = p.k_cache[l], *vc = p.v_cache[l];
-    const uint32_t nblk = (pos >> 3) + 1;
+    const uint32_t nblk = (pos >> 2) + 1;                                 // 4-key blocks in [0, pos]
+    const uint32_t mine = nblk > wave ? (nblk - wave + kCW - 1) / kCW : 0;  // this wave's blocks
     float *raw = c.xa + 2560, *qs = c.xa, *pm = c.xa + 384, *pl_ = c.xa + 400, *po = c.xa + 512;
     uint16_t *kn = (uint16_t *)(c.xa + 256), *vn = (uint16_t *)(c.xa + 320);
+    const uint32_t last = pos ? pos - 1 : 0u;  // kept rows before pos exist; pos arrives in LDS
 
     // Kept rows of earlier positions: the first kPre blocks of this wave, now.
-    u32x4 kk[kPre][2], vv[kPre][2];
+    u32x4 kk[kPre], vv[kPre];
 #pragma unroll
     for (int i = 0; i < kPre; i++) {
-        const uint32_t key = min(8 * (wave + kCW * i) + kj, pos ? pos - 1 : 0u);
+        const uint32_t key = min(4 * (wave + kCW * i) + kr, last);
         const uint64_t row = ((uint64_t)c.tbl[key >> shift] << shift) | (key & mask);
-        const size_t e = (row * Hkv + a) * 128 + 16 * part;
-        kk[i][0] = *(const u32x4 *)(kc + e);
-        kk[i][1] = *(const u32x4 *)(kc + e + 8);
-        vv[i][0] = *(const u32x4 *)(vc + e);
-        vv[i][1] = *(const u32x4 *)(vc + e + 8);
+        const size_t e = (row * Hkv + a) * 128 + 8 * part;
+        kk[i] = *(const u32x4 *)(kc + e);
+        vv[i] = *(const u32x4 *)(vc + e);
     }
     float ga = 0.0f, gb = 0.0f;
     if (wave < 2) { ga = p.q_norm[l][lane]; gb = p.q_norm[l][lane + 64]; }
     if (wave == 2) { ga = p.k_norm[l][lane]; gb = p.k_norm[l][lane + 64]; }
     const float2 cs = ((const float2 *)p.rope)[(size_t)pos * 64 + lane];
-    // q heads 2a, 2a + 1, then k and v of head a: 512 words in 4 runs of 128.
+    AMARK(1);
+    // q heads 2a, 2a + 1, then k and v of head a: 512 words in 4 runs of 128,
+    // at most two per thread, both loads in flight together.
     {
         const uint64_t *blk = p.hand + hd.qkv + (size_t)l * hd.block;
-        for (uint32_t i = c.tid; i < 512; i += kCT) {
-            const uint32_t r = i >> 7, d = i & 127;
-            const uint32_t gi = r < 2 ? a * 256 + i : (r == 2 ? pl.QD + a * 128 + d : pl.QD + (Hkv + a) * 128 + d);
-            uint64_t w = ld_tag(blk + gi), t0 = 0;
-            uint32_t it = 0;
-            while ((uint32_t)(w >> 32) != tag && spin(c, it, t0)) w = ld_tag(blk + gi);
-            raw[i] = __uint_as_float((uint32_t)w);
+        uint32_t gi[2];
+        uint64_t w[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const uint32_t i = min(c.tid + kCT * k, 511u), r = i >> 7, d = i & 127;
+            gi[k] = r < 2 ? a * 256 + i : (r == 2 ? pl.QD + a * 128 + d : pl.QD + (Hkv + a) * 128 + d);
+            w[k] = ld_tag(blk + gi[k]);
         }
+        uint64_t t0 = 0;
+        uint32_t it = 0;
+        while (((uint32_t)(w[0] >> 32) != tag || (uint32_t)(w[1] >> 32) != tag) && spin(c, it, t0)) {
+#pragma unroll
+            for (int k = 0; k < 2; k++)
+                if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(blk + gi[k]);
+        }
+        raw[c.tid] = __uint_as_float((uint32_t)w[0]);
+        if (c.tid + kCT < 512) raw[c.tid + kCT] = __uint_as_float((uint32_t)w[1]);
     }
+    AMARK(2);
     bar();  // 1
+    AMARK(3);
     if (wave < 4) {
         float x0 = raw[wave * 128 + lane], x1 = raw[wave * 128 + lane + 64];
         if (wave < 3) norm_rope(x0, x1, ga, gb, cs.x, cs.y, p.eps);
@@ -388,111 +428,100 @@ TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, C
         }
     }
     bar();  // 2
+    AMARK(4);
 
-    float q[2][16];
+    float q[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const float4 t0 = *(const float4 *)&qs[h * 128 + 8 * part], t1 = *(const float4 *)&qs[h * 128 + 8 * part + 4];
+        q[h][0] = t0.x; q[h][1] = t0.y; q[h][2] = t0.z; q[h][3] = t0.w;
+        q[h][4] = t1.x; q[h][5] = t1.y; q[h][6] = t1.z; q[h][7] = t1.w;
+    }
+    const u32x4 knew = *(const u32x4 *)(kn + 8 * part), vnew = *(const u32x4 *)(vn + 8 * part);
+    float m[2] = {-INFINITY, -INFINITY}, ls[2] = {0.0f, 0.0f}, o[2][8];
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int e = 0; e < 16; e += 4) {
-            const float4 t = *(const float4 *)&qs[h * 128 + 16 * part + e];
-            q[h][e] = t.x; q[h][e + 1] = t.y; q[h][e + 2] = t.z; q[h][e + 3] = t.w;
-        }
-    float m[2] = {-INFINITY, -INFINITY}, ls[2] = {0.0f, 0.0f};
-    float o[2][16];
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) o[h][e] = 0.0f;
+        for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
 
-    for (uint32_t i = 0;; i++) {
-        const uint32_t b = wave + kCW * i;
-        if (b >= nblk) break;
-        const uint32_t key = 8 * b + kj;
-        u32x4 k0, k1, v0, v1;
-        if (i < (uint32_t)kPre) {
-            k0 = kk[0][0]; k1 = kk[0][1]; v0 = vv[0][0]; v1 = vv[0][1];
+    for (uint32_t i0 = 0; i0 < mine; i0 += kPre) {
+        if (i0) {  // later passes (contexts past kCW kPre blocks): load this pass now
 #pragma unroll
-            for (int t = 1; t < kPre; t++)
-                if (i == (uint32_t)t) { k0 = kk[t][0]; k1 = kk[t][1]; v0 = vv[t][0]; v1 = vv[t][1]; }
-        } else {
-            const uint32_t kc_ = min(key, pos ? pos - 1 : 0u);
-            const uint64_t row = ((uint64_t)c.tbl[kc_ >> shift] << shift) | (kc_ & mask);
-            const size_t e = (row * Hkv + a) * 128 + 16 * part;
-            k0 = *(const u32x4 *)(kc + e);
-            k1 = *(const u32x4 *)(kc + e + 8);
-            v0 = *(const u32x4 *)(vc + e);
-            v1 = *(const u32x4 *)(vc + e + 8);
+            for (int i = 0; i < kPre; i++) {
+                const uint32_t key = min(4 * (wave + kCW * (i0 + i)) + kr, last);
+                const uint64_t row = ((uint64_t)c.tbl[key >> shift] << shift) | (key & mask);
+                const size_t e = (row * Hkv + a) * 128 + 8 * part;
+                kk[i] = *(const u32x4 *)(kc + e);
+                vv[i] = *(const u32x4 *)(vc + e);
+            }
         }
-        if (key == pos) {
-            k0 = *(const u32x4 *)(kn + 16 * part);
-            k1 = *(const u32x4 *)(kn + 16 * part + 8);
-            v0 = *(const u32x4 *)(vn + 16 * part);
-            v1 = *(const u32x4 *)(vn + 16 * part + 8);
-        }
-        const bool valid = key <= pos;
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-        float s0 = 0.0f, s1 = 0.0f;
+        float s[kPre][2];
+        bool ok[kPre];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float lo = lo_bf16(kw[e]), hi = hi_bf16(kw[e]);
-            s0 += q[0][2 * e] * lo;
-            s0 += q[0][2 * e + 1] * hi;
-            s1 += q[1][2 * e] * lo;
-            s1 += q[1][2 * e + 1] * hi;
+        for (int i = 0; i < kPre; i++) {
+            const uint32_t key = 4 * (wave + kCW * (i0 + i)) + kr;
+            ok[i] = key <= pos;  // past the wave's blocks too: key >= 4 nblk > pos
+            const u32x4 kv = key == pos ? knew : kk[i];
+            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+            float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const float lo = lo_bf16(kw[e]), hi = hi_bf16(kw[e]);
+                s0 += q[0][2 * e] * lo;
+                s0 += q[0][2 * e + 1] * hi;
+                s1 += q[1][2 * e] * lo;
+                s1 += q[1][2 * e + 1] * hi;
+            }
+            s[i][0] = ok[i] ? row16_sum(s0) * p.scale : -INFINITY;
+            s[i][1] = ok[i] ? row16_sum(s1) * p.scale : -INFINITY;
         }
-        float pk[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            float s = h == 0 ? s0 : s1;
-            s += __shfl_xor(s, 1, 64);
-            s += __shfl_xor(s, 2, 64);
-            s += __shfl_xor(s, 4, 64);
-            const float si = valid ? s * p.scale : -INFINITY;
-            float bm = fmaxf(si, __shfl_xor(si, 8, 64));
-            bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-            const float mn = fmaxf(m[h], bm);
-            const float alpha = mn == -INFINITY ? 1.0f : expf(m[h] - mn);
-            pk[h] = valid ? expf(si - mn) : 0.0f;
-            ls[h] = ls[h] * alpha + wave_sum(part == 0 ? pk[h] : 0.0f);
+            float bm = s[0][h];
+#pragma unroll
+            for (int i = 1; i < kPre; i++) bm = fmaxf(bm, s[i][h]);
+            const float mn = fmaxf(m[h], rows4_max(bm));  // finite: key 4 wave <= pos
+            const float alpha = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn);
+            float acc[8], sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kPre; i++) {
+                const float pk = ok[i] ? expf(s[i][h] - mn) : 0.0f;
+                sum += pk;
+                const u32x4 vx = (4 * (wave + kCW * (i0 + i)) + kr) == pos ? vnew : vv[i];
+                const uint32_t vw[4] = {ok[i] ? vx.x : 0u, ok[i] ? vx.y : 0u, ok[i] ? vx.z : 0u, ok[i] ? vx.w : 0u};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    acc[2 * e] += pk * lo_bf16(vw[e]);
+                    acc[2 * e + 1] += pk * hi_bf16(vw[e]);
+                }
+            }
+            ls[h] = ls[h] * alpha + rows4_sum(sum);
             m[h] = mn;
 #pragma unroll
-            for (int e = 0; e < 16; e++) o[h][e] *= alpha;
-        }
-        const uint32_t vw[8] = {valid ? v0.x : 0u, valid ? v0.y : 0u, valid ? v0.z : 0u, valid ? v0.w : 0u,
-                                valid ? v1.x : 0u, valid ? v1.y : 0u, valid ? v1.z : 0u, valid ? v1.w : 0u};
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const float lo = lo_bf16(vw[e]), hi = hi_bf16(vw[e]);
-            o[0][2 * e] += pk[0] * lo;
-            o[0][2 * e + 1] += pk[0] * hi;
-            o[1][2 * e] += pk[1] * lo;
-            o[1][2 * e + 1] += pk[1] * hi;
+            for (int e = 0; e < 8; e++) o[h][e] = o[h][e] * alpha + acc[e];
         }
     }
+    AMARK(5);
+    // Sum the four key rows; lanes of row 0 hold the wave's 2 x 128 partial sums.
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-            float v = o[h][e];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            o[h][e] = v;
+        for (int e = 0; e < 8; e++) o[h][e] = rows4_sum(o[h][e]);
+    if (kr == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            *(float4 *)&po[(wave * 2 + h) * 128 + 8 * part] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+            *(float4 *)&po[(wave * 2 + h) * 128 + 8 * part + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
         }
-    if (kj == 0) {
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int e = 0; e < 16; e += 4)
-                *(float4 *)&po[(wave * 2 + h) * 128 + 16 * part + e] =
-                    make_float4(o[h][e], o[h][e + 1], o[h][e + 2], o[h][e + 3]);
     }
     if (lane == 0) {
         pm[wave * 2] = m[0]; pm[wave * 2 + 1] = m[1];
         pl_[wave * 2] = ls[0]; pl_[wave * 2 + 1] = ls[1];
     }
     bar();  // 3
+    AMARK(6);
     if (c.tid < 256) {
         const uint32_t h = c.tid >> 7, d = c.tid & 127;
         float M = -INFINITY;
@@ -505,7 +534,9 @@ TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, C
         }
         st_tag(p.hand + hd.att + (size_t)l * hd.block + (a * 2 + h) * 128 + d, __float_as_uint(O / L), tag);
     }
+    AMARK(7);
     bar();  // 4: the next phase stages its input over this scratch
+    AMARK(8);
 }
 
 TS_DEV void better(float &bv, uint32_t &bi, float v, uint32_t i) {
@@ -518,13 +549,6 @@ TS_DEV void wave_best(float &bv, uint32_t &bi) {
         const uint32_t i = __shfl_xor(bi, o, 64);
         better(bv, bi, v, i);
     }
-}
-
-// Optional phase stamps of the first step (thread 0 of every group): slot 2 ph
-// when the phase's input is staged, 2 ph + 1 when its outputs are stored, 8 when
-// the group's attention is done; row L: lm_head input, chunks done, token.
-TS_DEV void mark(const DecodeStepArgs &p, const Ctx &c, uint32_t g, uint32_t t, uint32_t l, uint32_t k) {
-    if (p.marks && t == 0 && c.tid == 0) p.marks[((size_t)g * (p.L + 2) + l) * 10 + k] = now();
 }
 
 // One product phase of a layer.
@@ -747,33 +771,40 @@ struct Dma {
         seg_u = 0;
     }
 
-    // Issue every unit the ring has room for.
-    TS_DEV void issue() {
-        while (U < total && U < freed + kRing) {
-            while (seg_u >= seg_n) {
+    // Issue the next units the ring has room for: at least those below `need`, else
+    // at most kBurst of this wave's per barrier (a long burst would hold the barrier
+    // up; the compute meets a dozen barriers per layer).
+    TS_DEV void issue(uint32_t need) {
+        const uint32_t limit = min(total, min(freed + kRing, max(U + 2 * kBurst, need)));
+        while (U < limit) {
+            if (seg_u >= seg_n) {
                 seg++;
                 open_segment();
+                continue;
             }
-            if ((U & 1) == dw) {
+            const uint32_t n = min(seg_n - seg_u, limit - U);
+            // this wave's units of the run: U + k with (U + k) % 2 == dw
+            for (uint32_t k = (U & 1) == dw ? 0u : 1u; k < n; k += 2) {
                 if (inflight >= kMaxOut) {
                     wait_vm(kMaxOut - 8);
                     inflight = kMaxOut - 8;
                 }
-                const uint32_t off = min(seg_u * 1024 + lane * 16, seg_bytes - 16);
+                const uint32_t off = min((seg_u + k) * 1024 + lane * 16, seg_bytes - 16);
                 __builtin_amdgcn_global_load_lds((const void *)(seg_base + off),
-                                                 (lds_void *)(uintptr_t)(ring + ((U & (kRing - 1)) << 10)), 16, 0, 0);
+                                                 (lds_void *)(uintptr_t)(ring + (((U + k) & (kRing - 1)) << 10)), 16,
+                                                 0, 0);
                 mine++;
                 inflight++;
             }
-            seg_u++;
-            U++;
+            seg_u += n;
+            U += n;
         }
     }
 
     // The barrier after which the compute reads units [0, need) and before which it
     // has released units [0, free).
     TS_DEV void barrier(uint32_t need, uint32_t free) {
-        issue();
+        issue(need);  // every unit below `need` is issued (the ring holds a phase)
         const uint32_t below = dw == 0 ? (need + 1) >> 1 : need >> 1;  // this wave's units < need
         const uint32_t after = mine - min(mine, below);
         if (after < inflight) {
