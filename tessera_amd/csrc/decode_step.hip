@@ -749,7 +749,7 @@ struct Dma {
 
     TS_DEV void open_segment() {
         const DecodeStepArgs &a = *p;
-        const uint32_t per = 5 * a.L + pl.chunks, js = seg % per, H = a.H, F = a.F;
+        const uint32_t per = 5 * a.L + pl.chunks, js = __builtin_amdgcn_readfirstlane(seg % per), H = a.H, F = a.F;
         if (js < 5 * a.L) {
             const uint32_t l = js / 5, s = js % 5;
             if (s == 0) {
@@ -858,7 +858,12 @@ TS_DEV void dma(const DecodeStepArgs &p, uint32_t g, uint32_t dw, uint32_t lane,
 
 __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeStepArgs p) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = blockIdx.x;
+    // The wave index is uniform: readfirstlane lets the compiler keep what derives
+    // from it (the DMA cursors, the segment pointers) in scalar registers; as
+    // vector values, the per-layer pointer loads of the DMA waves became vector
+    // loads followed by a wait for every load in flight.
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63,
+                   g = blockIdx.x;
     volatile uint32_t *ctl = (volatile uint32_t *)(lds + kCtlOff);
     uint32_t *tbl = (uint32_t *)(lds + kTblOff);
     if (tid < 16) ctl[tid] = 0u;
