@@ -27,9 +27,8 @@
 //    schedule of barriers as the compute waves: before the barrier that starts a
 //    phase they wait (vmcnt) for that phase's rows, after the barrier that ends it
 //    they reuse its ring slots. Ring occupancy is known, never signalled;
-//  * the first kv_heads groups also run the attention of one kv head each (both q
-//    heads of the GQA pair), with the kept rows of earlier positions loaded before
-//    the q/k/v hand-off arrives;
+//  * the first q_heads groups also run the attention of one q head each, with
+//    the kept rows of earlier positions loaded before the q/k/v hand-off arrives;
 //  * the lm_head rows stream through the same ring in chunks; every group publishes
 //    its (max, index), and every group reduces all of them, so the next step's
 //    token needs no extra hand-off.
@@ -348,17 +347,20 @@ TS_DEV float rows4_max(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// Attention of kv head `a` (its two q heads) at position pos over kept rows
+// Attention of q head `h` (kv head a = h / 2) at position pos over kept rows
 // [0, pos] (engine/ir/interp/src/cpu.rs:141-167, 293-351): the raw q/k/v rows
 // come from the qkv hand-off; q and the new k are normalized and rotated, the new
-// k and v rows are appended (bf16), and the two heads' outputs are published.
+// k and v rows are appended (bf16, by the even head of the pair), and the head's
+// output is published. One group per q head: the two heads of a GQA pair run
+// side by side on two CUs (each loads the pair's kept rows) instead of one
+// after the other on one.
 // Lanes: key = lane / 16 of a 4-key block, dims 8 (lane % 16) .. +8; a wave takes
 // blocks wave + kCW i, kPre of them per softmax pass (one max and one sum per pass,
 // then the running (max, sum, acc) rescaled once per pass).
-TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, Ctx &c, uint32_t l, uint32_t a,
+TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, Ctx &c, uint32_t l, uint32_t h,
                       uint32_t pos, uint32_t tag) {
-    const uint32_t lane = c.lane, wave = c.wave;
-#define AMARK(k) do { if (l == 5 && tag == p.epoch) mark(p, c, a, 0, p.L + 1, k); } while (0)
+    const uint32_t lane = c.lane, wave = c.wave, a = h >> 1;
+#define AMARK(k) do { if (l == 5 && tag == p.epoch) mark(p, c, h, 0, p.L + 1, k); } while (0)
     AMARK(0);
     const uint32_t kr = lane >> 4, part = lane & 15;
     const uint32_t Hkv = p.Hkv, shift = p.page_shift, mask = (1u << shift) - 1;
@@ -380,69 +382,61 @@ TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, C
         vv[i] = *(const u32x4 *)(vc + e);
     }
     float ga = 0.0f, gb = 0.0f;
-    if (wave < 2) { ga = p.q_norm[l][lane]; gb = p.q_norm[l][lane + 64]; }
-    if (wave == 2) { ga = p.k_norm[l][lane]; gb = p.k_norm[l][lane + 64]; }
+    if (wave == 0) { ga = p.q_norm[l][lane]; gb = p.q_norm[l][lane + 64]; }
+    if (wave == 1) { ga = p.k_norm[l][lane]; gb = p.k_norm[l][lane + 64]; }
     const float2 cs = ((const float2 *)p.rope)[(size_t)pos * 64 + lane];
     AMARK(1);
-    // q heads 2a, 2a + 1, then k and v of head a: 512 words in 4 runs of 128,
-    // at most two per thread, both loads in flight together.
-    {
+    // q head h, then k and v of head a: 384 words in 3 runs of 128, one per thread.
+    static_assert(kCT >= 384, "one hand-off word per thread");
+    if (c.tid < 384) {
         const uint64_t *blk = p.hand + hd.qkv + (size_t)l * hd.block;
-        uint32_t gi[2];
-        uint64_t w[2];
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const uint32_t i = min(c.tid + kCT * k, 511u), r = i >> 7, d = i & 127;
-            gi[k] = r < 2 ? a * 256 + i : (r == 2 ? pl.QD + a * 128 + d : pl.QD + (Hkv + a) * 128 + d);
-            w[k] = ld_tag(blk + gi[k]);
-        }
+        const uint32_t r = c.tid >> 7, d = c.tid & 127;
+        const uint32_t gi = r == 0 ? h * 128 + d : (r == 1 ? pl.QD + a * 128 + d : pl.QD + (Hkv + a) * 128 + d);
+        uint64_t w = ld_tag(blk + gi);
         uint64_t t0 = 0;
         uint32_t it = 0;
-        while (((uint32_t)(w[0] >> 32) != tag || (uint32_t)(w[1] >> 32) != tag) && spin(c, it, t0)) {
-#pragma unroll
-            for (int k = 0; k < 2; k++)
-                if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(blk + gi[k]);
-        }
-        raw[c.tid] = __uint_as_float((uint32_t)w[0]);
-        if (c.tid + kCT < 512) raw[c.tid + kCT] = __uint_as_float((uint32_t)w[1]);
+        while ((uint32_t)(w >> 32) != tag && spin(c, it, t0)) w = ld_tag(blk + gi);
+        raw[c.tid] = __uint_as_float((uint32_t)w);
     }
     AMARK(2);
     bar();  // 1
     AMARK(3);
-    if (wave < 4) {
+    if (wave < 3) {
         float x0 = raw[wave * 128 + lane], x1 = raw[wave * 128 + lane + 64];
-        if (wave < 3) norm_rope(x0, x1, ga, gb, cs.x, cs.y, p.eps);
-        if (wave < 2) {
-            qs[wave * 128 + lane] = x0;
-            qs[wave * 128 + lane + 64] = x1;
+        if (wave < 2) norm_rope(x0, x1, ga, gb, cs.x, cs.y, p.eps);
+        if (wave == 0) {
+            qs[lane] = x0;
+            qs[lane + 64] = x1;
         } else {
             const uint16_t b0 = bf16_bits(x0), b1 = bf16_bits(x1);
-            uint16_t *dst = wave == 2 ? kn : vn;
+            uint16_t *dst = wave == 1 ? kn : vn;
             dst[lane] = b0;
             dst[lane + 64] = b1;
-            // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198).
-            const uint64_t row = ((uint64_t)c.tbl[pos >> shift] << shift) | (pos & mask);
-            uint16_t *cache = (wave == 2 ? p.k_cache[l] : p.v_cache[l]) + (row * Hkv + a) * 128;
-            cache[lane] = b0;
-            cache[lane + 64] = b1;
+            // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198),
+            // written once per pair (the odd head computes the same row).
+            if ((h & 1) == 0) {
+                const uint64_t row = ((uint64_t)c.tbl[pos >> shift] << shift) | (pos & mask);
+                uint16_t *cache = (wave == 1 ? p.k_cache[l] : p.v_cache[l]) + (row * Hkv + a) * 128;
+                // Agent scope: the odd head reads this row at the next step from
+                // another CU (perhaps another XCD, whose L2 this store would miss).
+                __hip_atomic_store(cache + lane, b0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(cache + lane + 64, b1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     bar();  // 2
     AMARK(4);
 
-    float q[2][8];
-#pragma unroll
-    for (int h = 0; h < 2; h++) {
-        const float4 t0 = *(const float4 *)&qs[h * 128 + 8 * part], t1 = *(const float4 *)&qs[h * 128 + 8 * part + 4];
-        q[h][0] = t0.x; q[h][1] = t0.y; q[h][2] = t0.z; q[h][3] = t0.w;
-        q[h][4] = t1.x; q[h][5] = t1.y; q[h][6] = t1.z; q[h][7] = t1.w;
+    float q[8];
+    {
+        const float4 t0 = *(const float4 *)&qs[8 * part], t1 = *(const float4 *)&qs[8 * part + 4];
+        q[0] = t0.x; q[1] = t0.y; q[2] = t0.z; q[3] = t0.w;
+        q[4] = t1.x; q[5] = t1.y; q[6] = t1.z; q[7] = t1.w;
     }
     const u32x4 knew = *(const u32x4 *)(kn + 8 * part), vnew = *(const u32x4 *)(vn + 8 * part);
-    float m[2] = {-INFINITY, -INFINITY}, ls[2] = {0.0f, 0.0f}, o[2][8];
+    float m = -INFINITY, ls = 0.0f, o[8];
 #pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
+    for (int e = 0; e < 8; e++) o[e] = 0.0f;
 
     for (uint32_t i0 = 0; i0 < mine; i0 += kPre) {
         if (i0) {  // later passes (contexts past kCW kPre blocks): load this pass now
@@ -455,7 +449,7 @@ TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, C
                 vv[i] = *(const u32x4 *)(vc + e);
             }
         }
-        float s[kPre][2];
+        float sc[kPre];
         bool ok[kPre];
 #pragma unroll
         for (int i = 0; i < kPre; i++) {
@@ -463,76 +457,64 @@ TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, C
             ok[i] = key <= pos;  // past the wave's blocks too: key >= 4 nblk > pos
             const u32x4 kv = key == pos ? knew : kk[i];
             const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-            float s0 = 0.0f, s1 = 0.0f;
+            float s0 = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                const float lo = lo_bf16(kw[e]), hi = hi_bf16(kw[e]);
-                s0 += q[0][2 * e] * lo;
-                s0 += q[0][2 * e + 1] * hi;
-                s1 += q[1][2 * e] * lo;
-                s1 += q[1][2 * e + 1] * hi;
+                s0 += q[2 * e] * lo_bf16(kw[e]);
+                s0 += q[2 * e + 1] * hi_bf16(kw[e]);
             }
-            s[i][0] = ok[i] ? row16_sum(s0) * p.scale : -INFINITY;
-            s[i][1] = ok[i] ? row16_sum(s1) * p.scale : -INFINITY;
+            sc[i] = ok[i] ? row16_sum(s0) * p.scale : -INFINITY;
         }
+        float bm = sc[0];
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            float bm = s[0][h];
+        for (int i = 1; i < kPre; i++) bm = fmaxf(bm, sc[i]);
+        const float mn = fmaxf(m, rows4_max(bm));  // finite: key 4 wave <= pos
+        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+        float acc[8], sum = 0.0f;
 #pragma unroll
-            for (int i = 1; i < kPre; i++) bm = fmaxf(bm, s[i][h]);
-            const float mn = fmaxf(m[h], rows4_max(bm));  // finite: key 4 wave <= pos
-            const float alpha = m[h] == -INFINITY ? 0.0f : expf(m[h] - mn);
-            float acc[8], sum = 0.0f;
+        for (int e = 0; e < 8; e++) acc[e] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+        for (int i = 0; i < kPre; i++) {
+            const float pk = ok[i] ? expf(sc[i] - mn) : 0.0f;
+            sum += pk;
+            const u32x4 vx = (4 * (wave + kCW * (i0 + i)) + kr) == pos ? vnew : vv[i];
+            const uint32_t vw[4] = {ok[i] ? vx.x : 0u, ok[i] ? vx.y : 0u, ok[i] ? vx.z : 0u, ok[i] ? vx.w : 0u};
 #pragma unroll
-            for (int i = 0; i < kPre; i++) {
-                const float pk = ok[i] ? expf(s[i][h] - mn) : 0.0f;
-                sum += pk;
-                const u32x4 vx = (4 * (wave + kCW * (i0 + i)) + kr) == pos ? vnew : vv[i];
-                const uint32_t vw[4] = {ok[i] ? vx.x : 0u, ok[i] ? vx.y : 0u, ok[i] ? vx.z : 0u, ok[i] ? vx.w : 0u};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    acc[2 * e] += pk * lo_bf16(vw[e]);
-                    acc[2 * e + 1] += pk * hi_bf16(vw[e]);
-                }
+            for (int e = 0; e < 4; e++) {
+                acc[2 * e] += pk * lo_bf16(vw[e]);
+                acc[2 * e + 1] += pk * hi_bf16(vw[e]);
             }
-            ls[h] = ls[h] * alpha + rows4_sum(sum);
-            m[h] = mn;
-#pragma unroll
-            for (int e = 0; e < 8; e++) o[h][e] = o[h][e] * alpha + acc[e];
         }
+        ls = ls * alpha + rows4_sum(sum);
+        m = mn;
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[e] = o[e] * alpha + acc[e];
     }
     AMARK(5);
-    // Sum the four key rows; lanes of row 0 hold the wave's 2 x 128 partial sums.
+    // Sum the four key rows; lanes of row 0 hold the wave's 128 partial sums.
 #pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[h][e] = rows4_sum(o[h][e]);
+    for (int e = 0; e < 8; e++) o[e] = rows4_sum(o[e]);
     if (kr == 0) {
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            *(float4 *)&po[(wave * 2 + h) * 128 + 8 * part] = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-            *(float4 *)&po[(wave * 2 + h) * 128 + 8 * part + 4] = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
-        }
+        *(float4 *)&po[wave * 128 + 8 * part] = make_float4(o[0], o[1], o[2], o[3]);
+        *(float4 *)&po[wave * 128 + 8 * part + 4] = make_float4(o[4], o[5], o[6], o[7]);
     }
     if (lane == 0) {
-        pm[wave * 2] = m[0]; pm[wave * 2 + 1] = m[1];
-        pl_[wave * 2] = ls[0]; pl_[wave * 2 + 1] = ls[1];
+        pm[wave] = m;
+        pl_[wave] = ls;
     }
     bar();  // 3
     AMARK(6);
-    if (c.tid < 256) {
-        const uint32_t h = c.tid >> 7, d = c.tid & 127;
+    if (c.tid < 128) {
+        const uint32_t d = c.tid;
         float M = -INFINITY;
-        for (uint32_t w = 0; w < kCW; w++) M = fmaxf(M, pm[w * 2 + h]);
+        for (uint32_t w = 0; w < kCW; w++) M = fmaxf(M, pm[w]);
         float L = 0.0f, O = 0.0f;
         for (uint32_t w = 0; w < kCW; w++) {
-            const float f = pm[w * 2 + h] == -INFINITY ? 0.0f : expf(pm[w * 2 + h] - M);
-            L += pl_[w * 2 + h] * f;
-            O += po[(w * 2 + h) * 128 + d] * f;
+            const float f = pm[w] == -INFINITY ? 0.0f : expf(pm[w] - M);
+            L += pl_[w] * f;
+            O += po[w * 128 + d] * f;
         }
-        st_tag(p.hand + hd.att + (size_t)l * hd.block + (a * 2 + h) * 128 + d, __float_as_uint(O / L), tag);
+        st_tag(p.hand + hd.att + (size_t)l * hd.block + h * 128 + d, __float_as_uint(O / L), tag);
     }
     AMARK(7);
     bar();  // 4: the next phase stages its input over this scratch
@@ -635,7 +617,7 @@ TS_DEV void compute(const DecodeStepArgs &p, Ctx &c, uint32_t g) {
                          false};
                 }
                 run_phase(p, c, f, tag, tok, g, t, l, ph);
-                if (ph == 0 && g < p.Hkv) {
+                if (ph == 0 && g < p.Hq) {
                     attention(p, pl, hd, c, l, g, pos, tag);
                     mark(p, c, g, t, l, 8);
                 }
@@ -838,7 +820,7 @@ TS_DEV void dma(const DecodeStepArgs &p, uint32_t g, uint32_t dw, uint32_t lane,
             for (uint32_t ph = 0; ph < 4; ph++) {
                 d.barrier(ends[ph], 0);  // staged input; the phase's rows landed
                 d.barrier(0, ends[ph]);  // products done; its rows released
-                if (ph == 0 && g < p.Hkv)
+                if (ph == 0 && g < p.Hq)
                     for (uint32_t b = 0; b < kAttBars; b++) d.barrier(0, 0);
             }
             U += pl.layer;
@@ -867,7 +849,7 @@ __global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeStepArgs p)
     volatile uint32_t *ctl = (volatile uint32_t *)(lds + kCtlOff);
     uint32_t *tbl = (uint32_t *)(lds + kTblOff);
     if (tid < 16) ctl[tid] = 0u;
-    if (g < p.Hkv)
+    if (g < p.Hq)
         for (uint32_t i = tid; i < p.kept_pages; i += kThreads) tbl[i] = p.table[i];
     __syncthreads();
     if (wave >= kCW) {
@@ -902,7 +884,7 @@ int decode_step_supported(uint32_t H, uint32_t L, uint32_t Hq, uint32_t Hkv, uin
     uint32_t ng = 0;
     int rc = decode_step_groups(&ng);
     if (rc != TS_OK) return rc;
-    if (D != 128 || Hkv == 0 || Hq != 2 * Hkv || Hkv > ng || 2 * ng > 896) return 1;
+    if (D != 128 || Hkv == 0 || Hq != 2 * Hkv || Hq > ng || 2 * ng > 896) return 1;
     if (L > kStepMaxLayers || H > kMaxH || H % 8 || F % 8 || F > kMaxXa || Hq * 128 > kMaxXa) return 1;
     if (kept_pages > kMaxPages) return 1;
     // No group may own more than kRW kCW rows of a phase, and every phase's rows
