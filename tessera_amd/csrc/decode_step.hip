@@ -59,7 +59,10 @@ constexpr uint32_t kMaxXa = 3072;              // staged input floats (H, Hq*128
 constexpr uint32_t kMaxH = 1024;
 constexpr uint32_t kMaxPages = 512;
 constexpr uint64_t kTimeout = 200000000ull;    // 2 s of the 100 MHz clock
-constexpr int kNX = (kMaxXa + kCT - 1) / kCT;  // staged words per compute thread
+constexpr int kNX = (kMaxXa + kCT - 1) / kCT;  // staged words per compute thread (widest input)
+constexpr int kNH = (kMaxH + kCT - 1) / kCT;   // staged words per compute thread (hidden-wide input)
+constexpr uint32_t kMaxGroups = 448;           // groups the step supports (2 pick words each)
+constexpr int kNA = (2 * kMaxGroups + kCT - 1) / kCT;
 constexpr int kPre = 7;                        // 4-key blocks per wave loaded before q arrives
 static_assert(kCW >= 4 && kCW <= 8, "attention uses waves 0..3 and LDS partials for up to 8 waves");
 
@@ -173,12 +176,15 @@ TS_DEV bool spin(Ctx &c, uint32_t &it, uint64_t &t0) {
     return true;
 }
 
-// Tagged words src[tid + kCT k] (k < kNX, index < n) into v[k]: every load is
-// issued, then the loads whose epoch is stale are reissued until none is.
-TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[kNX]) {
-    uint64_t w[kNX];
+// Tagged words src[tid + kCT k] (k < NX, index < n) into v[k]: every load is
+// issued, then the loads whose epoch is stale are reissued until none is. (A
+// second round of loads kept in flight measured slower: it doubles the polling
+// traffic every group puts on the memory system.)
+template <int NX>
+TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[NX]) {
+    uint64_t w[NX];
 #pragma unroll
-    for (int k = 0; k < kNX; k++) {
+    for (int k = 0; k < NX; k++) {
         const uint32_t i = c.tid + kCT * k;
         w[k] = i < n ? ld_tag(src + i) : ((uint64_t)tag << 32);
     }
@@ -187,14 +193,14 @@ TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&
     for (;;) {
         bool ready = true;
 #pragma unroll
-        for (int k = 0; k < kNX; k++) ready &= (uint32_t)(w[k] >> 32) == tag;
+        for (int k = 0; k < NX; k++) ready &= (uint32_t)(w[k] >> 32) == tag;
         if (ready || !spin(c, it, t0)) break;
 #pragma unroll
-        for (int k = 0; k < kNX; k++)
+        for (int k = 0; k < NX; k++)
             if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(src + c.tid + kCT * k);
     }
 #pragma unroll
-    for (int k = 0; k < kNX; k++) v[k] = __uint_as_float((uint32_t)w[k]);
+    for (int k = 0; k < NX; k++) v[k] = __uint_as_float((uint32_t)w[k]);
 }
 
 TS_DEV float dot8(u32x4 w, float4 a, float4 b, float acc) {
@@ -288,10 +294,11 @@ TS_DEV float row_value(const float *red, uint32_t r, uint32_t S) {
 // Stage an input vector of n <= 3072 values: xa[i] = v * g[i], xr[i] = v when
 // keep_raw, and the partial sums of squares of the RmsNorm; read back after the
 // next barrier by norm_inv.
-TS_DEV void stage(Ctx &c, const float (&v)[kNX], uint32_t n, const float (&g)[kNX], bool keep_raw) {
+template <int NX>
+TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX], bool keep_raw) {
     float ss = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kNX; k++) {
+    for (int k = 0; k < NX; k++) {
         const uint32_t i = c.tid + kCT * k;
         if (i < n) {
             c.xa[i] = v[k] * g[k];
@@ -545,11 +552,12 @@ struct Phase {
 
 // Stage the input, barrier (the DMA waves have landed the rows), products,
 // barrier, publish.
+template <int NX>
 TS_DEV void run_phase(const DecodeStepArgs &p, Ctx &c, const Phase &f, uint32_t tag, uint32_t tok, uint32_t g,
                       uint32_t t, uint32_t l, uint32_t ph) {
-    float v[kNX], gv[kNX];
+    float v[NX], gv[NX];
 #pragma unroll
-    for (int k = 0; k < kNX; k++) {
+    for (int k = 0; k < NX; k++) {
         const uint32_t i = c.tid + kCT * k;
         gv[k] = f.gain && i < f.n ? f.gain[i] : 1.0f;
     }
@@ -557,7 +565,7 @@ TS_DEV void run_phase(const DecodeStepArgs &p, Ctx &c, const Phase &f, uint32_t 
         poll(c, f.in, f.n, tag, v);
     } else {
 #pragma unroll
-        for (int k = 0; k < kNX; k++) {
+        for (int k = 0; k < NX; k++) {
             const uint32_t i = c.tid + kCT * k;
             v[k] = i < f.n ? bf16_float(p.embed[(size_t)tok * f.n + i]) : 0.0f;
         }
@@ -616,7 +624,10 @@ TS_DEV void compute(const DecodeStepArgs &p, Ctx &c, uint32_t g) {
                     f = {blk + hd.hf, nullptr, blk + hd.xo, F, Ud, pl.o.count, Ud, pl.o.count, F, pl.o.first, 1u,
                          false};
                 }
-                run_phase(p, c, f, tag, tok, g, t, l, ph);
+                if (ph & 1)
+                    run_phase<kNX>(p, c, f, tag, tok, g, t, l, ph);
+                else
+                    run_phase<kNH>(p, c, f, tag, tok, g, t, l, ph);
                 if (ph == 0 && g < p.Hq) {
                     attention(p, pl, hd, c, l, g, pos, tag);
                     mark(p, c, g, t, l, 8);
@@ -625,9 +636,9 @@ TS_DEV void compute(const DecodeStepArgs &p, Ctx &c, uint32_t g) {
         }
         // --- final RmsNorm, lm_head rows, greedy pick ---
         {
-            float v[kNX], gn[kNX];
+            float v[kNH], gn[kNH];
 #pragma unroll
-            for (int k = 0; k < kNX; k++) {
+            for (int k = 0; k < kNH; k++) {
                 const uint32_t i = c.tid + kCT * k;
                 gn[k] = i < H ? p.norm[i] : 1.0f;
             }
@@ -668,10 +679,10 @@ TS_DEV void compute(const DecodeStepArgs &p, Ctx &c, uint32_t g) {
             st_tag(am + 2 * g + 1, bi, tag);
         }
         {
-            float v[kNX];
+            float v[kNA];
             poll(c, am, 2 * p.NG, tag, v);
 #pragma unroll
-            for (int k = 0; k < kNX; k++)
+            for (int k = 0; k < kNA; k++)
                 if (c.tid + kCT * k < 2 * p.NG) c.red[128 + c.tid + kCT * k] = v[k];
         }
         bar();
@@ -884,7 +895,7 @@ int decode_step_supported(uint32_t H, uint32_t L, uint32_t Hq, uint32_t Hkv, uin
     uint32_t ng = 0;
     int rc = decode_step_groups(&ng);
     if (rc != TS_OK) return rc;
-    if (D != 128 || Hkv == 0 || Hq != 2 * Hkv || Hq > ng || 2 * ng > 896) return 1;
+    if (D != 128 || Hkv == 0 || Hq != 2 * Hkv || Hq > ng || ng > kMaxGroups) return 1;
     if (L > kStepMaxLayers || H > kMaxH || H % 8 || F % 8 || F > kMaxXa || Hq * 128 > kMaxXa) return 1;
     if (kept_pages > kMaxPages) return 1;
     // No group may own more than kRW kCW rows of a phase, and every phase's rows
