@@ -1,14 +1,18 @@
 """Headline benchmark: Qwen3-0.6B-shaped bf16 decode at batch 1 on one MI355X.
 
-A "step" is one greedy decode token (all 28 layers, the tied lm_head and argmax)
-replayed from the runner's HIP graph, with weights, kept rows and the token already
-resident in HBM. The timed run is the C1 workload: a 128-token prompt (seed 1), then
+A "step" is one greedy decode token (all 28 layers, the tied lm_head and argmax),
+run by the persistent decode step (one cooperative launch for all K steps), with
+weights, kept rows and the token already resident in HBM. The timed run is the C1 workload: a 128-token prompt (seed 1), then
 K decode steps (K=32: context 128..160). Warmup runs W steps of an earlier
 generation first. Prints one JSON line.
 
 Also measured in the same run:
-  * roofline of the dominant kernel (lanes on the lm_head shape: 151936 x 1024 bf16,
-    311 MB per launch) timed with HIP events on the stream it runs on;
+  * roofline of the dominant kernel: the persistent step itself (the decode call's
+    only kernel), its algorithmic bytes (every weight once per token + the kept rows
+    read) over its duration from HIP events on the runner's stream around the timed
+    launch; traffic from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes;
+  * the graph path's lm_head kernel (lanes, 151936 x 1024 bf16) against HBM
+    (extra.graph_lm_head);
   * the whole step against HBM: 1,192,099,840 weight bytes + 114,688 B per kept
     position per token;
   * prefill GEMMs (M=2048, the C2 projection shapes) as a fraction of bf16 MFMA peak;
@@ -47,6 +51,8 @@ def parse():
     p.add_argument("--no-rows", action="store_true", help="skip the C3/C4/C5 measurements")
     p.add_argument("--rows-only", action="store_true",
                    help="run only the C3/C4/C5 measurements (for kernel traces of those rows)")
+    p.add_argument("--decode-only", action="store_true",
+                   help="only the decode measurement (and a 256 MiB copy: the PMC yardstick)")
     p.add_argument("--roofline-only", action="store_true",
                    help="run only the lm_head lanes kernel and a plain copy of known size "
                         "(the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
@@ -84,6 +90,23 @@ def lm_head_roofline(torch, reps=20):
             "frac": nbytes / t / HBM_PEAK, "traffic": traffic,
             "kernel": "ts::gemv_kernel<1,8,f32 x,bf16 w> (lanes, lm_head 151936x1024, fused RmsNorm)",
             "bytes_per_launch": nbytes, "us_per_launch": t * 1e6}
+
+
+def decode_roofline(m, steps, mean_ctx):
+    """The persistent step over the timed decode call: one launch, `steps` tokens."""
+    ms = m.decode_ms
+    if ms <= 0:
+        return None
+    nbytes = int(steps * (WEIGHT_BYTES + KV_BYTES_PER_POS * mean_ctx))
+    t = ms / 1e3
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "decode_step_traffic.json")
+    if os.path.exists(prof):
+        traffic = int(json.load(open(prof))["traffic_bytes_per_token"] * steps)
+    return {"bound": "hbm", "achieved": nbytes / t / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+            "frac": nbytes / t / HBM_PEAK, "traffic": traffic,
+            "kernel": "ts::decode_step_kernel (persistent greedy step: 28 layers, lm_head, pick; one launch)",
+            "bytes_per_launch": nbytes, "us_per_launch": ms * 1e3, "steps_per_launch": steps}
 
 
 def copy_reference(torch, nbytes=256 << 20, reps=5):
@@ -324,8 +347,14 @@ def main():
     tok_s = a.steps / dt
     mean_ctx = PROMPT + (a.steps + 1) / 2
     step_bytes = WEIGHT_BYTES + KV_BYTES_PER_POS * mean_ctx
-    roof = lm_head_roofline(torch)
-    extra = {"step_hbm_frac": round(step_bytes * tok_s / HBM_PEAK, 4),
+    roof = decode_roofline(m, a.steps, mean_ctx)
+    if a.decode_only:
+        copy_reference(torch)
+        print(json.dumps({"value": round(tok_s, 2), "roofline": roof}), flush=True)
+        m.close()
+        return
+    extra = {"graph_lm_head": lm_head_roofline(torch),
+             "step_hbm_frac": round(step_bytes * tok_s / HBM_PEAK, 4),
              "step_bytes": int(step_bytes),
              "roofline_tok_s": round(HBM_PEAK / step_bytes, 1),
              "tokens_head": [int(t) for t in toks[:8]]}

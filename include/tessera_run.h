@@ -79,6 +79,12 @@ int tessera_qwen3_set_step(ts_qwen3 *m, int on);
 /* 1 when decode runs the persistent step. */
 int tessera_qwen3_step_mode(ts_qwen3 *m);
 
+/* Device time (ms) of the last tessera_qwen3_decode call's steps, from HIP events
+ * recorded on the runner's stream around the persistent launch (or the graph
+ * replays); -1 when the call was not timed. No counterpart in the reference
+ * (its runner reports wall time, engine/plan/run/src/device.rs:227-245). */
+float tessera_qwen3_decode_ms(ts_qwen3 *m);
+
 /* Debug: the persistent step writes phase stamps (100 MHz clock) of the first
  * step of each later launch to `marks` (device memory of groups * (layers + 2)
  * * 10 words; NULL stops it); *groups receives the grid size. */

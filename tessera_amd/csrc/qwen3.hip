@@ -102,6 +102,8 @@ struct ts_qwen3 {
     uint32_t *d_error = nullptr;
     uint32_t epoch = 1, groups = 0;
     uint64_t *step_marks = nullptr;  // debug: phase stamps of the next persistent launch
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last decode call's device work
+    float decode_ms = -1.0f;
 
     template <class T>
     int alloc(T **p, size_t count) {
@@ -382,6 +384,8 @@ extern "C" void tessera_qwen3_close(ts_qwen3 *m) {
     if (m->stream) hipStreamSynchronize(m->stream);
     if (m->graph) hipGraphExecDestroy(m->graph);
     for (void *p : m->allocs) hipFree(p);
+    if (m->ev0) (void)hipEventDestroy(m->ev0);
+    if (m->ev1) (void)hipEventDestroy(m->ev1);
     if (m->stream) hipStreamDestroy(m->stream);
     if (m->pool) tessera_kv_free(m->pool);
     delete m;
@@ -460,6 +464,13 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
                "qwen3_decode: %u steps from position %u pass the kept context %u", steps, m->position,
                m->c.max_context);
     hipError_t e;
+    if (!m->ev0) {
+        e = hipEventCreate(&m->ev0);
+        if (e == hipSuccess) e = hipEventCreate(&m->ev1);
+        if (e != hipSuccess) return ts::hip_status(e, "hipEventCreate");
+    }
+    const bool timed = steps > 0 && (m->use_step || m->graph || !m->use_graph);
+    if (timed && (e = hipEventRecord(m->ev0, m->stream)) != hipSuccess) return ts::hip_status(e, "hipEventRecord");
     if (m->use_step && steps > 0) {
         TRY(launch_step(m, steps));
     } else if (m->use_graph && !m->graph && steps > 0) {
@@ -485,6 +496,7 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
             TRY(decode_step(m));
         }
     }
+    if (timed && (e = hipEventRecord(m->ev1, m->stream)) != hipSuccess) return ts::hip_status(e, "hipEventRecord");
     const uint32_t first = m->position;
     m->position += steps;
     if (tokens_out && steps) {
@@ -493,6 +505,9 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
     }
     e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) return ts::hip_status(e, "decode");
+    m->decode_ms = -1.0f;
+    if (timed && (e = hipEventElapsedTime(&m->decode_ms, m->ev0, m->ev1)) != hipSuccess)
+        return ts::hip_status(e, "hipEventElapsedTime");
     if (m->use_step && steps > 0) {
         uint32_t err = 0;
         e = hipMemcpy(&err, m->d_error, 4, hipMemcpyDeviceToHost);
@@ -528,6 +543,11 @@ extern "C" int tessera_qwen3_set_step(ts_qwen3 *m, int on) {
 }
 
 extern "C" int tessera_qwen3_step_mode(ts_qwen3 *m) { return m && m->use_step ? 1 : 0; }
+
+// Device time of the last decode call's steps (HIP events on the runner's stream
+// around the persistent launch or the graph replays), ms; -1 when not timed
+// (a first graph call also captures and instantiates the graph).
+extern "C" float tessera_qwen3_decode_ms(ts_qwen3 *m) { return m ? m->decode_ms : -1.0f; }
 
 // Debug: the persistent step records phase stamps into `marks` (device memory,
 // groups * (layers + 2) * 10 words) on its next launches; NULL stops it.

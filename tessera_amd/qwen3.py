@@ -33,6 +33,7 @@ SIGNATURES = {
     "tessera_qwen3_set_graph": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_set_step": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_step_mode": (C.c_int, [_P]),
+    "tessera_qwen3_decode_ms": (C.c_float, [_P]),
     "tessera_qwen3_step_marks": (C.c_int, [_P, _P, C.POINTER(C.c_uint32)]),
     "tessera_qwen3_stream": (_P, [_P]),
     "tessera_qwen3_position": (C.c_uint32, [_P]),
@@ -116,6 +117,11 @@ class Qwen3:
     def set_step(self, on: bool):
         """True: decode as one persistent launch per call; False: the graph of kernels."""
         abi.check(self.L.tessera_qwen3_set_step(self.h, 1 if on else 0), "tessera_qwen3_set_step")
+
+    @property
+    def decode_ms(self) -> float:
+        """Device time of the last decode call's steps (HIP events), ms; -1 if untimed."""
+        return float(self.L.tessera_qwen3_decode_ms(self.h))
 
     @property
     def step_mode(self) -> bool:
