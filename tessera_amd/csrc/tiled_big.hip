@@ -87,7 +87,7 @@ TS_DEV void mfma_step(const BigParams &p, char *lds, uint32_t s, f32x4 (&acc)[8]
 #pragma unroll
         for (int i = 0; i < 8; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[i][j] = mfma16(af[ks][i], bfr[ks][j], acc[i][j]);
+            for (int j = 0; j < 4; j++) acc[i][j] = mfma16(bfr[ks][j], af[ks][i], acc[i][j]);
     // Masks: 0x008 MFMA, 0x020 VMEM read, 0x100 DS read.
     __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);
 #pragma unroll
@@ -140,24 +140,47 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_big_kernel(BigParams p) {
     }
     mfma_step<false>(p, lds, steps - 1, acc, m0, n0, wave, lane, wm, wn, col, grp);
 
-    // Epilogue. D lane layout: column col, rows 4*grp + r of each 16x16 tile.
+    // Epilogue. The MFMA operands are swapped (weights first), so lane l holds row
+    // col of each 16x16 tile and its four adjacent columns 4 grp .. + 3: one 8-byte
+    // (bf16) or 16-byte (f32) store per lane and tile instead of four 2-byte ones
+    // (the scattered stores took a fifth of the lm_head product's time).
     const uint32_t N = p.n, M = p.m;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < 8; i++) {
+        const uint32_t m = m0 + wm * 128 + i * 16 + col;
+        if (m >= M) continue;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t m = m0 + wm * 128 + i * 16 + 4 * grp + r;
-            if (m >= M) continue;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t n = n0 + wn * 64 + j * 16 + col;
-                if (n >= N) continue;
-                float v = acc[i][j][r];
-                if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
-                if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
-                else ((float *)p.out)[(size_t)m * N + n] = v;
+        for (int j = 0; j < 4; j++) {
+            const uint32_t n = n0 + wn * 64 + j * 16 + 4 * grp;
+            if (n >= N) continue;
+            const size_t e = (size_t)m * N + n;
+            f32x4 v = acc[i][j];
+            const bool whole = n + 3 < N && (e & 3) == 0;
+            if (p.stages & TS_AFTER_ADD) {
+                if (whole) {
+                    v += *(const f32x4 *)(p.a0 + e);
+                } else {
+                    for (uint32_t r = 0; r < 4 && n + r < N; r++) v[r] += p.a0[e + r];
+                }
+            }
+            if (p.out_bf16) {
+                uint16_t *o = (uint16_t *)p.out + e;
+                if (whole) {
+                    *(u32x2 *)o = u32x2{(uint32_t)bf16_bits(v[0]) | ((uint32_t)bf16_bits(v[1]) << 16),
+                                        (uint32_t)bf16_bits(v[2]) | ((uint32_t)bf16_bits(v[3]) << 16)};
+                } else {
+                    for (uint32_t r = 0; r < 4 && n + r < N; r++) o[r] = bf16_bits(v[r]);
+                }
+            } else {
+                float *o = (float *)p.out + e;
+                if (whole) {
+                    *(f32x4 *)o = v;
+                } else {
+                    for (uint32_t r = 0; r < 4 && n + r < N; r++) o[r] = v[r];
+                }
             }
         }
+    }
 }
 
 }  // namespace
