@@ -26,7 +26,8 @@
 
 namespace {
 
-constexpr int kRows = 64;   // query rows per group
+constexpr int kQT = 1;              // 16-query tiles per wave
+constexpr int kRows = 64 * kQT;     // query rows per group (4 waves)
 constexpr int kKeys = 32;   // keys per block
 
 struct FlashParams {
@@ -79,6 +80,16 @@ TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t
     }
 }
 
+// Lane exchanges within octets / quads on the VALU (DPP), not LDS permutes.
+TS_DEV uint32_t xor1(uint32_t x) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false); }
+TS_DEV uint32_t xor2(uint32_t x) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false); }
+// lane j of an octet takes lane j ^ 4: the octet mirrored (j -> 7 - j), then the
+// quad reversed (j -> j ^ 3).
+TS_DEV uint32_t xor4(uint32_t x) {
+    const int m = __builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);
+}
+
 // 8 x 8 transpose of bf16 across the 8 lanes of an octet: lane j holds row j (8 values
 // in 4 words) in, column j out. Three butterfly stages swap the off-diagonal blocks
 // between lanes j and j ^ 4, j ^ 2, j ^ 1.
@@ -87,20 +98,20 @@ TS_DEV u32x4 transpose8(u32x4 v, uint32_t j) {
     {  // lanes ^ 4: words {2, 3} of the low lane <-> words {0, 1} of the high lane
         const bool up = j & 4;
         const uint32_t s0 = up ? w[0] : w[2], s1 = up ? w[1] : w[3];
-        const uint32_t r0 = __shfl_xor(s0, 4), r1 = __shfl_xor(s1, 4);
+        const uint32_t r0 = xor4(s0), r1 = xor4(s1);
         if (up) { w[0] = r0; w[1] = r1; } else { w[2] = r0; w[3] = r1; }
     }
     {  // lanes ^ 2: words {1, 3} of the low lane <-> words {0, 2} of the high lane
         const bool up = j & 2;
         const uint32_t s0 = up ? w[0] : w[1], s1 = up ? w[2] : w[3];
-        const uint32_t r0 = __shfl_xor(s0, 2), r1 = __shfl_xor(s1, 2);
+        const uint32_t r0 = xor2(s0), r1 = xor2(s1);
         if (up) { w[0] = r0; w[2] = r1; } else { w[1] = r0; w[3] = r1; }
     }
     {  // lanes ^ 1: the high halves of the low lane <-> the low halves of the high lane
         const bool up = j & 1;
         const uint32_t s0 = up ? (w[0] & 0xffffu) | (w[1] << 16) : (w[0] >> 16) | (w[1] & 0xffff0000u);
         const uint32_t s1 = up ? (w[2] & 0xffffu) | (w[3] << 16) : (w[2] >> 16) | (w[3] & 0xffff0000u);
-        const uint32_t r0 = __shfl_xor(s0, 1), r1 = __shfl_xor(s1, 1);
+        const uint32_t r0 = xor1(s0), r1 = xor1(s1);
         if (up) {
             w[0] = (w[0] & 0xffff0000u) | (r0 & 0xffffu);
             w[1] = (w[1] & 0xffff0000u) | (r0 >> 16);
@@ -116,15 +127,37 @@ TS_DEV u32x4 transpose8(u32x4 v, uint32_t j) {
     return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-// Byte offset of (d, 8-key group kg) in V^T: rows of 32 keys (64 bytes), 16-byte
-// groups XOR-swizzled by d / 4 so 16 consecutive d rows hit distinct banks.
-TS_DEV uint32_t vt_at(uint32_t d, uint32_t kg) { return d * 64 + ((kg ^ ((d >> 2) & 3)) << 4); }
+// Sums and maxima over the four 16-lane rows of a wave, in every lane (gfx950
+// permlane swaps: VALU).
+TS_DEV float rows4_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+TS_DEV float rows4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 
+// V^T in LDS: row d holds the block's 32 keys in the order the P^T operand uses:
+// key 16 t + 4 g + i (tile t, group g, i < 4) at position 8 g + 4 t + i, so lane
+// group g reads its 8 keys as one 16-byte chunk. Chunks XOR-swizzled by d / 4 so 16
+// consecutive d rows hit distinct banks. Byte offset of position q (a multiple of 4).
+TS_DEV uint32_t vt_at(uint32_t d, uint32_t q) { return d * 64 + ((((q >> 3) ^ ((d >> 2) & 3))) << 4) + (q & 7) * 2; }
+
+// The transposed formulation: S^T = K Q^T and O^T = V^T P^T. With K as the A
+// operand (rows = keys) and Q^T as B (columns = queries), the S^T accumulator lane
+// (query col, group g) holds keys 4 g + i of each 16-key tile: after the softmax
+// those P^T values are, packed as they are, the B operand of the P V product over
+// keys {4 g + i, 16 + 4 g + i} (no staging of P through LDS), and the O^T
+// accumulator gives each lane 4 adjacent d of its query (16-byte stores).
 template <bool QF32>
 __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
     __shared__ __attribute__((aligned(16))) char svt[128 * kKeys * 2];  // V transposed (vt_at)
-    __shared__ __attribute__((aligned(16))) uint16_t sp[4][QF32 ? 2 : 1][16][kKeys];  // P parts per wave
     __shared__ uint32_t srange[2];
     __shared__ uint32_t stab_s[kMaxPages];  // this group's page-table entries
 
@@ -133,10 +166,6 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
     const uint32_t h = blockIdx.y, G = p.heads / p.kv_heads, kvh = h / G;
     const uint32_t r0 = blockIdx.x * kRows;
     const uint32_t slot = p.slots[r0];
-
-    // This wave's rows: r0 + 16*wave + i. Row i's position for masking.
-    const uint32_t my_row = r0 + 16 * wave + col;  // A-operand row of this lane
-    const bool row_ok = my_row < p.rows;
 
     // Key range of the whole group: [lo, hi].
     if (t == 0) { srange[0] = 0xffffffffu; srange[1] = 0; }
@@ -158,48 +187,51 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
         stab = stab_s;
     }
 
-    // q operand, loaded once: bf16 q as is; f32 q as two exact bf16 parts.
-    u32x4 qh[4], ql[4];
-    if (!QF32) {
-        const uint16_t *qr = (const uint16_t *)p.q + ((size_t)(row_ok ? my_row : 0) * p.heads + h) * 128 + 32 * grp;
+    // This wave's queries: r0 + 16 kQT wave + 16 qt + col. The q operand
+    // (B, columns = queries), loaded once: lane group g holds d 32 g + 8 j .. + 8 for
+    // d-step j; bf16 q as is, f32 q as two exact bf16 parts.
+    u32x4 qh[kQT][4], ql[kQT][4];
+    uint32_t rpos[kQT], rfrom[kQT];
+    bool rlive[kQT];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            qh[j] = row_ok ? *(const u32x4 *)(qr + 8 * j) : u32x4{0, 0, 0, 0};
-            ql[j] = u32x4{0, 0, 0, 0};
-        }
-    } else {
-        const float *qr = (const float *)p.q + ((size_t)(row_ok ? my_row : 0) * p.heads + h) * 128 + 32 * grp;
+    for (int qt = 0; qt < kQT; qt++) {
+        const uint32_t r = r0 + 16 * kQT * wave + 16 * qt + col;
+        rlive[qt] = r < p.rows;
+        rpos[qt] = rlive[qt] ? p.positions[r] : 0;
+        rfrom[qt] = rpos[qt] > p.back ? rpos[qt] - p.back : 0;
+        if (!QF32) {
+            const uint16_t *qr = (const uint16_t *)p.q + ((size_t)(rlive[qt] ? r : 0) * p.heads + h) * 128 + 32 * grp;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            uint32_t hh[4], ll[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                float a = row_ok ? qr[8 * j + 2 * e] : 0.0f, b = row_ok ? qr[8 * j + 2 * e + 1] : 0.0f;
-                float ha = bf16_round(a), hb = bf16_round(b);
-                hh[e] = pack_bf16x2(ha, hb);
-                ll[e] = pack_bf16x2(a - ha, b - hb);
+            for (int j = 0; j < 4; j++) {
+                qh[qt][j] = rlive[qt] ? *(const u32x4 *)(qr + 8 * j) : u32x4{0, 0, 0, 0};
+                ql[qt][j] = u32x4{0, 0, 0, 0};
             }
-            qh[j] = u32x4{hh[0], hh[1], hh[2], hh[3]};
-            ql[j] = u32x4{ll[0], ll[1], ll[2], ll[3]};
-        }
-    }
-    // Positions of the 4 rows this lane holds in the S/D layout (rows 4*grp + i).
-    uint32_t rpos[4], rfrom[4];
-    bool rlive[4];
+        } else {
+            const float *qr = (const float *)p.q + ((size_t)(rlive[qt] ? r : 0) * p.heads + h) * 128 + 32 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t r = r0 + 16 * wave + 4 * grp + i;
-        rlive[i] = r < p.rows;
-        rpos[i] = rlive[i] ? p.positions[r] : 0;
-        rfrom[i] = rpos[i] > p.back ? rpos[i] - p.back : 0;
+            for (int j = 0; j < 4; j++) {
+                uint32_t hh[4], ll[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    float a = rlive[qt] ? qr[8 * j + 2 * e] : 0.0f, b = rlive[qt] ? qr[8 * j + 2 * e + 1] : 0.0f;
+                    float ha = bf16_round(a), hb = bf16_round(b);
+                    hh[e] = pack_bf16x2(ha, hb);
+                    ll[e] = pack_bf16x2(a - ha, b - hb);
+                }
+                qh[qt][j] = u32x4{hh[0], hh[1], hh[2], hh[3]};
+                ql[qt][j] = u32x4{ll[0], ll[1], ll[2], ll[3]};
+            }
+        }
     }
 
-    float m[4], l[4];
+    float m[kQT], l[kQT];
 #pragma unroll
-    for (int i = 0; i < 4; i++) { m[i] = -INFINITY; l[i] = 0.0f; }
-    f32x4 o[8];
+    for (int qt = 0; qt < kQT; qt++) { m[qt] = -INFINITY; l[qt] = 0.0f; }
+    f32x4 o[kQT][8];  // O^T: [query tile][d tile], lane: query col, d 4 grp + i
 #pragma unroll
-    for (int d = 0; d < 8; d++) o[d] = f32x4{0, 0, 0, 0};
+    for (int qt = 0; qt < kQT; qt++)
+#pragma unroll
+        for (int d = 0; d < 8; d++) o[qt][d] = f32x4{0, 0, 0, 0};
 
     u32x4 kr[2], vr[2];
     fetch_kv(p, slot, kvh, lo, hi, stab, p0, kr, vr);
@@ -211,80 +243,98 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
             const uint32_t idx = t + 256 * c2, key = idx >> 4, chunk = idx & 15;
             *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c2];
             // V: after the octet transpose lane j holds d = 8 vchunk + j for keys
-            // 8 kg .. 8 kg + 7: one 16-byte write.
-            const uint32_t g = 2 * wave + c2, vchunk = 8 * (g >> 2) + (lane >> 3);
-            *(u32x4 *)(svt + vt_at(vchunk * 8 + (lane & 7), g & 3)) = transpose8(vr[c2], lane & 7);
+            // 8 kg .. 8 kg + 7, which sit at positions q0 .. q0 + 3 and q0 + 8 .. + 11.
+            const uint32_t g = 2 * wave + c2, kg = g & 3, vchunk = 8 * (g >> 2) + (lane >> 3);
+            const uint32_t d = vchunk * 8 + (lane & 7), q0 = 16 * (kg & 1) + 4 * (kg >> 1);
+            const u32x4 tv = transpose8(vr[c2], lane & 7);
+            *(u32x2 *)(svt + vt_at(d, q0)) = u32x2{tv.x, tv.y};
+            *(u32x2 *)(svt + vt_at(d, q0 + 8)) = u32x2{tv.z, tv.w};
         }
         // The next block's loads fly while this one computes (the barrier below
         // waits for LDS only).
         if (kb + kKeys <= hi) fetch_kv(p, slot, kvh, kb + kKeys, hi, stab, p0, kr, vr);
         lds_barrier();
 
-        // S for two 16-key tiles.
-        f32x4 s[2];
+        // S^T for two 16-key tiles x two query tiles.
+        f32x4 s[2][kQT];
 #pragma unroll
         for (int kt = 0; kt < 2; kt++) {
-            s[kt] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int qt = 0; qt < kQT; qt++) s[kt][qt] = f32x4{0, 0, 0, 0};
             const uint32_t key = kt * 16 + col;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t chunk = grp * 4 + j;  // d [32*grp + 8j, +8): q's order
+                const uint32_t chunk = grp * 4 + j;  // d [32 grp + 8 j, +8): q's order
                 const bf16x8 kf = as_bf16x8(*(const u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8]);
-                s[kt] = mfma16(as_bf16x8(qh[j]), kf, s[kt]);
-                if (QF32) s[kt] = mfma16(as_bf16x8(ql[j]), kf, s[kt]);
+#pragma unroll
+                for (int qt = 0; qt < kQT; qt++) {
+                    s[kt][qt] = mfma16(kf, as_bf16x8(qh[qt][j]), s[kt][qt]);
+                    if (QF32) s[kt][qt] = mfma16(kf, as_bf16x8(ql[qt][j]), s[kt][qt]);
+                }
             }
         }
-        // Online softmax per row; write P parts for the A layout.
+        // Online softmax per query (a lane's column), over its 8 keys and the
+        // lanes of its column in the other three row groups.
+        bf16x8 ph[kQT], pl[kQT];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float sv[2];
+        for (int qt = 0; qt < kQT; qt++) {
+            float sv[2][4];
             float mx = -INFINITY;
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const uint32_t kpos = kb + kt * 16 + col;
-                const bool ok = rlive[i] && kpos <= rpos[i] && kpos >= rfrom[i];
-                sv[kt] = ok ? s[kt][i] * p.scale : -INFINITY;
-                mx = fmaxf(mx, sv[kt]);
-            }
-            mx = row16_max(mx);
-            const float mn = fmaxf(m[i], mx);
-            const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
+            for (int kt = 0; kt < 2; kt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t kpos = kb + kt * 16 + 4 * grp + i;
+                    const bool ok = rlive[qt] && kpos <= rpos[qt] && kpos >= rfrom[qt];
+                    sv[kt][i] = ok ? s[kt][qt][i] * p.scale : -INFINITY;
+                    mx = fmaxf(mx, sv[kt][i]);
+                }
+            mx = rows4_max(mx);
+            const float mn = fmaxf(m[qt], mx);
+            const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[qt] - mn);
             float sum = 0.0f;
+            uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++) {
-                const float pv = (sv[kt] == -INFINITY) ? 0.0f : expf(sv[kt] - mn);
-                sum += pv;
-                const float ph = bf16_round(pv);
-                sp[wave][0][4 * grp + i][kt * 16 + col] = bf16_bits(ph);
-                if (QF32) sp[wave][QF32 ? 1 : 0][4 * grp + i][kt * 16 + col] = bf16_bits(pv - ph);
-            }
-            sum = row16_sum(sum);
-            l[i] = l[i] * alpha + sum;
-            m[i] = mn;
+            for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-            for (int d = 0; d < 8; d++) o[d][i] *= alpha;
+                for (int i = 0; i < 4; i += 2) {
+                    const float pa = (sv[kt][i] == -INFINITY) ? 0.0f : expf(sv[kt][i] - mn);
+                    const float pb = (sv[kt][i + 1] == -INFINITY) ? 0.0f : expf(sv[kt][i + 1] - mn);
+                    sum += pa;
+                    sum += pb;
+                    const float ha = bf16_round(pa), hb = bf16_round(pb);
+                    hw[2 * kt + i / 2] = pack_bf16x2(ha, hb);
+                    lw[2 * kt + i / 2] = pack_bf16x2(pa - ha, pb - hb);
+                }
+            ph[qt] = as_bf16x8(u32x4{hw[0], hw[1], hw[2], hw[3]});
+            pl[qt] = as_bf16x8(u32x4{lw[0], lw[1], lw[2], lw[3]});
+            sum = rows4_sum(sum);
+            l[qt] = l[qt] * alpha + sum;
+            m[qt] = mn;
+#pragma unroll
+            for (int d = 0; d < 8; d++) o[qt][d] *= alpha;
         }
-        // P (rows x 32 keys) as the A operand: lane row col, keys 8*grp..+8. sp[wave]
-        // is this wave's own: its LDS operations run in order, no barrier needed.
-        const bf16x8 ph = as_bf16x8(*(const u32x4 *)&sp[wave][0][col][8 * grp]);
-        const bf16x8 pl = as_bf16x8(*(const u32x4 *)&sp[wave][QF32 ? 1 : 0][col][8 * grp]);
+        // O^T += V^T P^T: A = V^T rows d, keys in P^T's order (one 16-byte read).
 #pragma unroll
         for (int d = 0; d < 8; d++) {
-            const bf16x8 vf = as_bf16x8(*(const u32x4 *)(svt + vt_at(d * 16 + col, grp)));
-            o[d] = mfma16(ph, vf, o[d]);
-            if (QF32) o[d] = mfma16(pl, vf, o[d]);
+            const bf16x8 vf = as_bf16x8(*(const u32x4 *)(svt + vt_at(d * 16 + col, 8 * grp)));
+#pragma unroll
+            for (int qt = 0; qt < kQT; qt++) {
+                o[qt][d] = mfma16(vf, ph[qt], o[qt][d]);
+                if (QF32) o[qt][d] = mfma16(vf, pl[qt], o[qt][d]);
+            }
         }
     }
 
-    // O / l. D layout: column (d) col of tile d, rows 4*grp + i.
+    // O / l: lane (query col of tile qt) holds d = 16 dt + 4 grp + i.
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        if (!rlive[i]) continue;
-        const uint32_t r = r0 + 16 * wave + 4 * grp + i;
+    for (int qt = 0; qt < kQT; qt++) {
+        if (!rlive[qt]) continue;
+        const uint32_t r = r0 + 16 * kQT * wave + 16 * qt + col;
         float *dst = p.out + ((size_t)r * p.heads + h) * 128;
-        const float inv = 1.0f / l[i];
+        const float inv = 1.0f / l[qt];
 #pragma unroll
-        for (int d = 0; d < 8; d++) dst[d * 16 + col] = o[d][i] * inv;
+        for (int d = 0; d < 8; d++) *(f32x4 *)(dst + d * 16 + 4 * grp) = o[qt][d] * inv;
     }
 }
 
