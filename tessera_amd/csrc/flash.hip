@@ -10,7 +10,7 @@
 // gfx950 design:
 //  * One 256-thread group per (64 query rows, head); each wave owns 16 rows.
 //    The 64 rows must belong to one slot (the prefill shape: runs of one slot).
-//  * Keys stream in 32-row blocks. K goes to LDS as rows ([key][d], 16-byte chunks
+//  * Keys stream in 64-row blocks. K goes to LDS as rows ([key][d], 16-byte chunks
 //    XOR-swizzled by key). V goes to LDS transposed ([d][key]) so the P*V operand is
 //    one 16-byte read per lane: each lane octet loads an 8 keys x 8 d block,
 //    transposes it across the octet with lane shuffles and writes 16 bytes per lane
@@ -28,7 +28,8 @@ namespace {
 
 constexpr int kQT = 1;              // 16-query tiles per wave
 constexpr int kRows = 64 * kQT;     // query rows per group (4 waves)
-constexpr int kKeys = 32;   // keys per block
+constexpr int kKeys = 64;   // keys per block (two 32-key MFMA steps of P V)
+constexpr int kC = kKeys * 16 / 256;  // 16-byte K (and V) loads per thread and block
 
 struct FlashParams {
     const void *q;
@@ -54,28 +55,28 @@ TS_DEV uint64_t key_row(const FlashParams &p, uint32_t slot, uint32_t pos, const
                 : kept_row(p, slot, pos);
 }
 
-// K and V of one 32-key block in flight, 16 bytes (8 d values) per load. K: thread t
+// K and V of one 64-key block in flight, 16 bytes (8 d values) per load. K: thread t
 // holds key idx / 16, chunk idx % 16 (idx = t + 256 c). V: wave w's load c covers keys
-// 8 kg + (l & 7) and chunks 8 cg + (l >> 3), g = 2w + c, kg = g & 3, cg = g >> 2, so
-// each lane octet holds an 8 keys x 8 d block for the transpose in stage_v. Keys past
-// the last row's position may sit in pages never written: they load as zeros.
+// 8 kg + (l & 7) and chunks 8 cg + (l >> 3), g = kC w + c, kg = g & 7, cg = g >> 3, so
+// each lane octet holds an 8 keys x 8 d block for the octet transpose. Keys past the
+// last row's position may sit in pages never written: they load as zeros.
 TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t kb, uint32_t hi, const uint32_t *stab,
-                     uint32_t p0, u32x4 (&kr)[2], u32x4 (&vr)[2]) {
+                     uint32_t p0, u32x4 (&kr)[kC], u32x4 (&vr)[kC]) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int c2 = 0; c2 < 2; c2++) {
-        const uint32_t idx = threadIdx.x + 256 * c2, key = idx >> 4, chunk = idx & 15, pos = kb + key;
-        kr[c2] = u32x4{0, 0, 0, 0};
+    for (int c = 0; c < kC; c++) {
+        const uint32_t idx = threadIdx.x + 256 * c, key = idx >> 4, chunk = idx & 15, pos = kb + key;
+        kr[c] = u32x4{0, 0, 0, 0};
         if (pos <= hi && (p.table || pos < p.keys)) {
             const uint64_t row = key_row(p, slot, pos, stab, p0);
-            kr[c2] = *(const u32x4 *)(p.k + (row * p.kv_heads + kvh) * 128 + chunk * 8);
+            kr[c] = *(const u32x4 *)(p.k + (row * p.kv_heads + kvh) * 128 + chunk * 8);
         }
-        const uint32_t g = 2 * wave + c2, vkey = 8 * (g & 3) + (lane & 7), vchunk = 8 * (g >> 2) + (lane >> 3);
+        const uint32_t g = kC * wave + c, vkey = 8 * (g & 7) + (lane & 7), vchunk = 8 * (g >> 3) + (lane >> 3);
         const uint32_t vpos = kb + vkey;
-        vr[c2] = u32x4{0, 0, 0, 0};
+        vr[c] = u32x4{0, 0, 0, 0};
         if (vpos <= hi && (p.table || vpos < p.keys)) {
             const uint64_t row = key_row(p, slot, vpos, stab, p0);
-            vr[c2] = *(const u32x4 *)(p.v + (row * p.kv_heads + kvh) * 128 + vchunk * 8);
+            vr[c] = *(const u32x4 *)(p.v + (row * p.kv_heads + kvh) * 128 + vchunk * 8);
         }
     }
 }
@@ -142,17 +143,18 @@ TS_DEV float rows4_max(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// V^T in LDS: row d holds the block's 32 keys in the order the P^T operand uses:
-// key 16 t + 4 g + i (tile t, group g, i < 4) at position 8 g + 4 t + i, so lane
-// group g reads its 8 keys as one 16-byte chunk. Chunks XOR-swizzled by d / 4 so 16
-// consecutive d rows hit distinct banks. Byte offset of position q (a multiple of 4).
-TS_DEV uint32_t vt_at(uint32_t d, uint32_t q) { return d * 64 + ((((q >> 3) ^ ((d >> 2) & 3))) << 4) + (q & 7) * 2; }
+// V^T in LDS: row d holds the block's 64 keys in the order the P^T operands use:
+// key 32 s + 16 t + 4 g + i (step s, tile t, group g, i < 4) at position
+// 32 s + 8 g + 4 t + i, so lane group g reads its 8 keys of step s as one 16-byte
+// chunk. Chunks XOR-swizzled by d % 8 so 8 consecutive d rows hit distinct banks.
+// Byte offset of position q (a multiple of 4).
+TS_DEV uint32_t vt_at(uint32_t d, uint32_t q) { return d * 128 + (((q >> 3) ^ (d & 7)) << 4) + (q & 7) * 2; }
 
 // The transposed formulation: S^T = K Q^T and O^T = V^T P^T. With K as the A
 // operand (rows = keys) and Q^T as B (columns = queries), the S^T accumulator lane
 // (query col, group g) holds keys 4 g + i of each 16-key tile: after the softmax
 // those P^T values are, packed as they are, the B operand of the P V product over
-// keys {4 g + i, 16 + 4 g + i} (no staging of P through LDS), and the O^T
+// keys {4 g + i, 16 + 4 g + i} of each 32-key step (no staging of P through LDS), and the O^T
 // accumulator gives each lane 4 adjacent d of its query (16-byte stores).
 template <bool QF32>
 __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
@@ -224,6 +226,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
         }
     }
 
+    const float sl = p.scale * 1.4426950408889634f;  // scores to base 2
     float m[kQT], l[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) { m[qt] = -INFINITY; l[qt] = 0.0f; }
@@ -233,20 +236,20 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
         for (int d = 0; d < 8; d++) o[qt][d] = f32x4{0, 0, 0, 0};
 
-    u32x4 kr[2], vr[2];
+    u32x4 kr[kC], vr[kC];
     fetch_kv(p, slot, kvh, lo, hi, stab, p0, kr, vr);
     for (uint32_t kb = lo; kb <= hi; kb += kKeys) {
         // Every wave is done reading the previous block's K and V^T.
         lds_barrier();
 #pragma unroll
-        for (int c2 = 0; c2 < 2; c2++) {
-            const uint32_t idx = t + 256 * c2, key = idx >> 4, chunk = idx & 15;
-            *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c2];
+        for (int c = 0; c < kC; c++) {
+            const uint32_t idx = t + 256 * c, key = idx >> 4, chunk = idx & 15;
+            *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c];
             // V: after the octet transpose lane j holds d = 8 vchunk + j for keys
-            // 8 kg .. 8 kg + 7, which sit at positions q0 .. q0 + 3 and q0 + 8 .. + 11.
-            const uint32_t g = 2 * wave + c2, kg = g & 3, vchunk = 8 * (g >> 2) + (lane >> 3);
-            const uint32_t d = vchunk * 8 + (lane & 7), q0 = 16 * (kg & 1) + 4 * (kg >> 1);
-            const u32x4 tv = transpose8(vr[c2], lane & 7);
+            // 8 kg .. 8 kg + 7 (step kg / 4), at positions q0 .. q0 + 3 and q0 + 8 .. + 11.
+            const uint32_t g = kC * wave + c, kg = g & 7, vchunk = 8 * (g >> 3) + (lane >> 3), ks = kg & 3;
+            const uint32_t d = vchunk * 8 + (lane & 7), q0 = 32 * (kg >> 2) + 16 * (ks & 1) + 4 * (ks >> 1);
+            const u32x4 tv = transpose8(vr[c], lane & 7);
             *(u32x2 *)(svt + vt_at(d, q0)) = u32x2{tv.x, tv.y};
             *(u32x2 *)(svt + vt_at(d, q0 + 8)) = u32x2{tv.z, tv.w};
         }
@@ -255,10 +258,10 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
         if (kb + kKeys <= hi) fetch_kv(p, slot, kvh, kb + kKeys, hi, stab, p0, kr, vr);
         lds_barrier();
 
-        // S^T for two 16-key tiles x two query tiles.
-        f32x4 s[2][kQT];
+        // S^T for four 16-key tiles x the query tiles.
+        f32x4 s[4][kQT];
 #pragma unroll
-        for (int kt = 0; kt < 2; kt++) {
+        for (int kt = 0; kt < 4; kt++) {
 #pragma unroll
             for (int qt = 0; qt < kQT; qt++) s[kt][qt] = f32x4{0, 0, 0, 0};
             const uint32_t key = kt * 16 + col;
@@ -273,55 +276,77 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
                 }
             }
         }
-        // Online softmax per query (a lane's column), over its 8 keys and the
-        // lanes of its column in the other three row groups.
-        bf16x8 ph[kQT], pl[kQT];
+        // Online softmax per query (a lane's column), over its 16 keys and the
+        // lanes of its column in the other three row groups, in base 2: scores are
+        // scaled by scale * log2(e) and exponentiated with v_exp_f32 (exp(x) =
+        // 2^(x log2 e)); m and l keep the base-2 running max and the sum.
+        // A block wholly inside every query's window of the wave skips the masks.
+        bool inside = true;
+#pragma unroll
+        for (int qt = 0; qt < kQT; qt++) inside &= !rlive[qt] || (kb + kKeys - 1 <= rpos[qt] && kb >= rfrom[qt]);
+        inside = __builtin_amdgcn_ballot_w64(!inside) == 0;  // uniform
+        bf16x8 ph[2][kQT], pl[2][kQT];
 #pragma unroll
         for (int qt = 0; qt < kQT; qt++) {
-            float sv[2][4];
+            float sv[4][4];
             float mx = -INFINITY;
+            const int hi_off = (int)rpos[qt] - (int)kb, lo_off = (int)rfrom[qt] - (int)kb;
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+            for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    const uint32_t kpos = kb + kt * 16 + 4 * grp + i;
-                    const bool ok = rlive[qt] && kpos <= rpos[qt] && kpos >= rfrom[qt];
-                    sv[kt][i] = ok ? s[kt][qt][i] * p.scale : -INFINITY;
+                    const int k = kt * 16 + 4 * (int)grp + i;
+                    const bool ok = inside || (rlive[qt] && k <= hi_off && k >= lo_off);
+                    sv[kt][i] = ok ? s[kt][qt][i] * sl : -INFINITY;
                     mx = fmaxf(mx, sv[kt][i]);
                 }
             mx = rows4_max(mx);
             const float mn = fmaxf(m[qt], mx);
-            const float alpha = (mn == -INFINITY) ? 1.0f : expf(m[qt] - mn);
+            const float alpha = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
+            const float mo = mn == -INFINITY ? 0.0f : mn;  // exp2(-inf - 0) = 0 for masked keys
             float sum = 0.0f;
-            uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int kt = 0; kt < 2; kt++)
+            for (int st = 0; st < 2; st++) {
+                uint32_t hw[4], lw[4];
 #pragma unroll
-                for (int i = 0; i < 4; i += 2) {
-                    const float pa = (sv[kt][i] == -INFINITY) ? 0.0f : expf(sv[kt][i] - mn);
-                    const float pb = (sv[kt][i + 1] == -INFINITY) ? 0.0f : expf(sv[kt][i + 1] - mn);
-                    sum += pa;
-                    sum += pb;
-                    const float ha = bf16_round(pa), hb = bf16_round(pb);
-                    hw[2 * kt + i / 2] = pack_bf16x2(ha, hb);
-                    lw[2 * kt + i / 2] = pack_bf16x2(pa - ha, pb - hb);
-                }
-            ph[qt] = as_bf16x8(u32x4{hw[0], hw[1], hw[2], hw[3]});
-            pl[qt] = as_bf16x8(u32x4{lw[0], lw[1], lw[2], lw[3]});
+                for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i += 2) {
+                        const int kt = 2 * st + tt;
+                        const float pa = __builtin_amdgcn_exp2f(sv[kt][i] - mo);
+                        const float pb = __builtin_amdgcn_exp2f(sv[kt][i + 1] - mo);
+                        sum += pa;
+                        sum += pb;
+                        hw[2 * tt + i / 2] = pack_bf16x2(pa, pb);
+                        if (QF32) {
+                            const float ha = bf16_float((uint16_t)(hw[2 * tt + i / 2] & 0xffffu));
+                            const float hb = bf16_float((uint16_t)(hw[2 * tt + i / 2] >> 16));
+                            lw[2 * tt + i / 2] = pack_bf16x2(pa - ha, pb - hb);
+                        } else {
+                            lw[2 * tt + i / 2] = 0u;
+                        }
+                    }
+                ph[st][qt] = as_bf16x8(u32x4{hw[0], hw[1], hw[2], hw[3]});
+                pl[st][qt] = as_bf16x8(u32x4{lw[0], lw[1], lw[2], lw[3]});
+            }
             sum = rows4_sum(sum);
             l[qt] = l[qt] * alpha + sum;
             m[qt] = mn;
 #pragma unroll
             for (int d = 0; d < 8; d++) o[qt][d] *= alpha;
         }
-        // O^T += V^T P^T: A = V^T rows d, keys in P^T's order (one 16-byte read).
+        // O^T += V^T P^T: A = V^T rows d, keys in P^T's order (one 16-byte read per
+        // 32-key step).
 #pragma unroll
         for (int d = 0; d < 8; d++) {
-            const bf16x8 vf = as_bf16x8(*(const u32x4 *)(svt + vt_at(d * 16 + col, 8 * grp)));
 #pragma unroll
-            for (int qt = 0; qt < kQT; qt++) {
-                o[qt][d] = mfma16(vf, ph[qt], o[qt][d]);
-                if (QF32) o[qt][d] = mfma16(vf, pl[qt], o[qt][d]);
+            for (int st = 0; st < 2; st++) {
+                const bf16x8 vf = as_bf16x8(*(const u32x4 *)(svt + vt_at(d * 16 + col, 32 * st + 8 * grp)));
+#pragma unroll
+                for (int qt = 0; qt < kQT; qt++) {
+                    o[qt][d] = mfma16(vf, ph[st][qt], o[qt][d]);
+                    if (QF32) o[qt][d] = mfma16(vf, pl[st][qt], o[qt][d]);
+                }
             }
         }
     }
