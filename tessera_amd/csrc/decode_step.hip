@@ -53,6 +53,7 @@ constexpr uint32_t kThreads = (kCW + kDW) * 64;
 constexpr uint32_t kRing = 128;                // ring units of 1 KiB
 constexpr uint32_t kMaxOut = 56;               // DMA loads in flight per wave (vmcnt holds 63)
 constexpr uint32_t kBurst = 8;                 // DMA loads a wave issues per barrier
+constexpr uint32_t kLmBurst = 24;              // the same in the lm_head chunks (7 us a token over 8)
 constexpr uint32_t kRW = 4;                    // product rows per compute wave
 constexpr uint32_t kChunk = kRW * kCW;         // lm_head rows per chunk
 constexpr uint32_t kMaxXa = 3072;              // staged input floats (H, Hq*128 and F)
@@ -736,6 +737,7 @@ struct Dma {
     uint32_t freed;      // units whose slots may be reused: unit u needs u < freed + kRing
     uint32_t mine;       // this wave's units issued so far
     uint32_t inflight;   // of those, possibly still in flight
+    uint32_t burst;      // loads per wave issued ahead of need per barrier
     // the segment under the cursor
     uint32_t seg, seg_u, seg_n, seg_bytes;
     const char *seg_base;
@@ -768,7 +770,7 @@ struct Dma {
     // at most kBurst of this wave's per barrier (a long burst would hold the barrier
     // up; the compute meets a dozen barriers per layer).
     TS_DEV void issue(uint32_t need) {
-        const uint32_t limit = min(total, min(freed + kRing, max(U + 2 * kBurst, need)));
+        const uint32_t limit = min(total, min(freed + kRing, max(U + 2 * burst, need)));
         while (U < limit) {
             if (seg_u >= seg_n) {
                 seg++;
@@ -821,6 +823,7 @@ TS_DEV void dma(const DecodeStepArgs &p, uint32_t g, uint32_t dw, uint32_t lane,
     d.freed = 0;
     d.mine = 0;
     d.inflight = 0;
+    d.burst = kBurst;
     d.seg = 0;
     d.open_segment();
     const Plan &pl = d.pl;
@@ -837,12 +840,16 @@ TS_DEV void dma(const DecodeStepArgs &p, uint32_t g, uint32_t dw, uint32_t lane,
             U += pl.layer;
         }
         d.barrier(pl.chunks ? U + chunk_units(p, pl, 0) : 0, 0);  // lm input; chunk 0 landed
+        // The lm_head chunks: little compute per barrier, so the DMA waves keep the
+        // ring as full as their loads in flight allow.
+        d.burst = kLmBurst;
         for (uint32_t ch = 0; ch < pl.chunks; ch++) {
             const uint32_t next = U + chunk_units(p, pl, ch);
             const uint32_t need = ch + 1 < pl.chunks ? next + chunk_units(p, pl, ch + 1) : 0;
             d.barrier(need, next);
             U = next;
         }
+        d.burst = kBurst;
         d.barrier(0, 0);
         d.barrier(0, 0);
     }
