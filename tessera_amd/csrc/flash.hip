@@ -8,7 +8,10 @@
 // [max(0, pos - back), pos] of its slot, p = softmax(dot(q, k) * scale).
 //
 // gfx950 design:
-//  * One 256-thread group per (64 query rows, head); each wave owns 16 rows.
+//  * One group per (64 query rows, q heads of one kv head): 4 waves per q head, each
+//    wave owns 16 rows; with GQA pairs a group of 8 waves covers both heads of the
+//    pair, so each K/V block is loaded and staged once for twice the MFMA work (the
+//    staging is VALU work, and VALU, not the matrix unit, bounds this kernel).
 //    The 64 rows must belong to one slot (the prefill shape: runs of one slot).
 //  * Keys stream in 64-row blocks. K goes to LDS as rows ([key][d], 16-byte chunks
 //    XOR-swizzled by key). V goes to LDS transposed ([d][key]) so the P*V operand is
@@ -16,10 +19,10 @@
 //    transposes it across the octet with lane shuffles and writes 16 bytes per lane
 //    (16-bit scattered writes bank-conflicted 16 ways and cost more than the MFMAs).
 //  * The group's page-table entries are copied to LDS once.
-//  * S = Q K^T: 2 key tiles x 4 d-steps of v_mfma_f32_16x16x32_bf16 per q part
-//    (bf16 q as is; f32 q split into two exact bf16 parts). Online softmax per row
-//    with 16-lane butterflies. P (bf16; two parts for f32 q) is staged through the
-//    wave's own LDS into the A layout; O[16 rows, 128] += P V in 8 MFMA column tiles.
+//  * S^T = K Q^T: 4 key tiles x 4 d-steps of v_mfma_f32_16x16x32_bf16 per q part
+//    (bf16 q as is; f32 q split into two exact bf16 parts). Online softmax per query
+//    in base 2; P^T (bf16; two parts for f32 q) feeds O^T += V^T P^T straight from
+//    registers (the layout notes at flash_rows_kernel).
 //  * The next key block's K/V loads are issued before the current block computes,
 //    and the barriers wait for LDS only, so HBM latency hides under the MFMAs.
 #include "common.h"
@@ -29,7 +32,6 @@ namespace {
 constexpr int kQT = 1;              // 16-query tiles per wave
 constexpr int kRows = 64 * kQT;     // query rows per group (4 waves)
 constexpr int kKeys = 64;   // keys per block (two 32-key MFMA steps of P V)
-constexpr int kC = kKeys * 16 / 256;  // 16-byte K (and V) loads per thread and block
 
 struct FlashParams {
     const void *q;
@@ -55,17 +57,19 @@ TS_DEV uint64_t key_row(const FlashParams &p, uint32_t slot, uint32_t pos, const
                 : kept_row(p, slot, pos);
 }
 
-// K and V of one 64-key block in flight, 16 bytes (8 d values) per load. K: thread t
-// holds key idx / 16, chunk idx % 16 (idx = t + 256 c). V: wave w's load c covers keys
+// K and V of one 64-key block in flight, 16 bytes (8 d values) per load, kC loads per
+// thread (1024 / kC threads). K: thread t holds key idx / 16, chunk idx % 16
+// (idx = t + 1024 / kC c). V: wave w's load c covers keys
 // 8 kg + (l & 7) and chunks 8 cg + (l >> 3), g = kC w + c, kg = g & 7, cg = g >> 3, so
 // each lane octet holds an 8 keys x 8 d block for the octet transpose. Keys past the
 // last row's position may sit in pages never written: they load as zeros.
+template <int kC>
 TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t kb, uint32_t hi, const uint32_t *stab,
                      uint32_t p0, u32x4 (&kr)[kC], u32x4 (&vr)[kC]) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int c = 0; c < kC; c++) {
-        const uint32_t idx = threadIdx.x + 256 * c, key = idx >> 4, chunk = idx & 15, pos = kb + key;
+        const uint32_t idx = threadIdx.x + 1024 / kC * c, key = idx >> 4, chunk = idx & 15, pos = kb + key;
         kr[c] = u32x4{0, 0, 0, 0};
         if (pos <= hi && (p.table || pos < p.keys)) {
             const uint64_t row = key_row(p, slot, pos, stab, p0);
@@ -156,8 +160,11 @@ TS_DEV uint32_t vt_at(uint32_t d, uint32_t q) { return d * 128 + (((q >> 3) ^ (d
 // those P^T values are, packed as they are, the B operand of the P V product over
 // keys {4 g + i, 16 + 4 g + i} of each 32-key step (no staging of P through LDS), and the O^T
 // accumulator gives each lane 4 adjacent d of its query (16-byte stores).
-template <bool QF32>
-__global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
+// HG q heads of one kv head per group (GQA): 4 HG waves, wave w on head h0 + w / 4; the
+// block's K and V are loaded and staged once for all of them.
+template <bool QF32, int HG>
+__global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
+    constexpr int kC = kKeys * 16 / (256 * HG);  // 16-byte K (and V) loads per thread and block
     __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
     __shared__ __attribute__((aligned(16))) char svt[128 * kKeys * 2];  // V transposed (vt_at)
     __shared__ uint32_t srange[2];
@@ -165,7 +172,8 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
-    const uint32_t h = blockIdx.y, G = p.heads / p.kv_heads, kvh = h / G;
+    const uint32_t G = p.heads / p.kv_heads, h = blockIdx.y * HG + (wave >> 2), kvh = h / G;
+    const uint32_t qw = wave & 3;  // the wave's 16 rows within the group's 64
     const uint32_t r0 = blockIdx.x * kRows;
     const uint32_t slot = p.slots[r0];
 
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
     const uint32_t p0 = p.table ? lo >> p.page_shift : 0, np = p.table ? (hi >> p.page_shift) - p0 + 1 : 0;
     const uint32_t *stab = nullptr;
     if (p.table && np <= kMaxPages) {
-        for (uint32_t i = t; i < np; i += 256) stab_s[i] = p.table[(uint64_t)slot * p.kept_pages + p0 + i];
+        for (uint32_t i = t; i < np; i += 256 * HG) stab_s[i] = p.table[(uint64_t)slot * p.kept_pages + p0 + i];
         __syncthreads();
         stab = stab_s;
     }
@@ -197,7 +205,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
     bool rlive[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) {
-        const uint32_t r = r0 + 16 * kQT * wave + 16 * qt + col;
+        const uint32_t r = r0 + 16 * kQT * qw + 16 * qt + col;
         rlive[qt] = r < p.rows;
         rpos[qt] = rlive[qt] ? p.positions[r] : 0;
         rfrom[qt] = rpos[qt] > p.back ? rpos[qt] - p.back : 0;
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
         lds_barrier();
 #pragma unroll
         for (int c = 0; c < kC; c++) {
-            const uint32_t idx = t + 256 * c, key = idx >> 4, chunk = idx & 15;
+            const uint32_t idx = t + 256 * HG * c, key = idx >> 4, chunk = idx & 15;
             *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c];
             // V: after the octet transpose lane j holds d = 8 vchunk + j for keys
             // 8 kg .. 8 kg + 7 (step kg / 4), at positions q0 .. q0 + 3 and q0 + 8 .. + 11.
@@ -317,7 +325,10 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
                         const float pb = __builtin_amdgcn_exp2f(sv[kt][i + 1] - mo);
                         sum += pa;
                         sum += pb;
-                        hw[2 * tt + i / 2] = pack_bf16x2(pa, pb);
+                        // p in [0, 1] (never NaN for finite scores): the plain
+                        // round-to-nearest-even conversion, no NaN fix-up.
+                        hw[2 * tt + i / 2] = __builtin_bit_cast(
+                            uint32_t, __builtin_convertvector(ts_f32x2{pa, pb}, ts_bf16x2));
                         if (QF32) {
                             const float ha = bf16_float((uint16_t)(hw[2 * tt + i / 2] & 0xffffu));
                             const float hb = bf16_float((uint16_t)(hw[2 * tt + i / 2] >> 16));
@@ -332,8 +343,11 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
             sum = rows4_sum(sum);
             l[qt] = l[qt] * alpha + sum;
             m[qt] = mn;
+            // Rescale O only when some query of the wave has a new maximum.
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
 #pragma unroll
-            for (int d = 0; d < 8; d++) o[qt][d] *= alpha;
+                for (int d = 0; d < 8; d++) o[qt][d] *= alpha;
+            }
         }
         // O^T += V^T P^T: A = V^T rows d, keys in P^T's order (one 16-byte read per
         // 32-key step).
@@ -355,7 +369,7 @@ __global__ __launch_bounds__(256) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) {
         if (!rlive[qt]) continue;
-        const uint32_t r = r0 + 16 * kQT * wave + 16 * qt + col;
+        const uint32_t r = r0 + 16 * kQT * qw + 16 * qt + col;
         float *dst = p.out + ((size_t)r * p.heads + h) * 128;
         const float inv = 1.0f / l[qt];
 #pragma unroll
@@ -385,8 +399,13 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
     p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads; p.back = a->back;
     p.kept_pages = a->kept_pages; p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
     p.scale = a->scale;
-    const auto kern = a->q_dtype == TS_F32 ? flash_rows_kernel<true> : flash_rows_kernel<false>;
-    hipLaunchKernelGGL(kern, dim3((a->rows + kRows - 1) / kRows, a->heads), dim3(256), 0, (hipStream_t)stream, p);
+    // Two q heads per group when the kv heads are shared in pairs (or more, evenly).
+    const int hg = (a->heads / a->kv_heads) % 2 == 0 ? 2 : 1;
+    const bool f32 = a->q_dtype == TS_F32;
+    const auto kern = hg == 2 ? (f32 ? flash_rows_kernel<true, 2> : flash_rows_kernel<false, 2>)
+                              : (f32 ? flash_rows_kernel<true, 1> : flash_rows_kernel<false, 1>);
+    hipLaunchKernelGGL(kern, dim3((a->rows + kRows - 1) / kRows, a->heads / hg), dim3(256 * hg), 0,
+                       (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("flash_rows launch");
     return TS_OK;
 }

@@ -128,8 +128,11 @@ def test_prefill_flash_rows_bf16_q(lens):
     np.testing.assert_allclose(got, want(c, s), atol=4e-3, rtol=0)
 
 
-def test_prefill_flash_window_and_gqa():
-    c = paged_case(8, [200], heads=8, kv_heads=2, pos=([0] * 200, list(range(200))))
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (4, 4), (6, 2)])
+def test_prefill_flash_window_and_gqa(heads, kv_heads):
+    """A window of 40 keys; q heads per kv head 4 (groups of 8 waves over two heads),
+    1 and 3 (groups of 4 waves over one head)."""
+    c = paged_case(8, [200], heads=heads, kv_heads=kv_heads, pos=([0] * 200, list(range(200))))
     np.testing.assert_allclose(run("flash", c, 0.25, back=40), want(c, 0.25, "back", 40), atol=ATOL, rtol=0)
 
 
