@@ -8,11 +8,14 @@
 // [max(0, pos - back), pos] of its slot, p = softmax(dot(q, k) * scale).
 //
 // gfx950 design:
-//  * One group per (64 query rows, q heads of one kv head): 4 waves per q head, each
-//    wave owns 16 rows; with GQA pairs a group of 8 waves covers both heads of the
-//    pair, so each K/V block is loaded and staged once for twice the MFMA work (the
-//    staging is VALU work, and VALU, not the matrix unit, bounds this kernel).
-//    The 64 rows must belong to one slot (the prefill shape: runs of one slot).
+//  * One group per (128 query rows, q heads of one kv head): 4 waves per q head, each
+//    wave owns 32 rows (two 16-query MFMA tiles); with GQA pairs a group of 8 waves
+//    covers both heads of the pair. Each K/V block is loaded and staged once for all
+//    of that MFMA work: the staging is VALU work, and VALU, not the matrix unit,
+//    bounds this kernel (64 rows and one head per group measured 1.8x slower).
+//  * Rows come in 64-row blocks of one slot (the prefill shape: runs of one slot).
+//    When the group's two 64-row halves belong to different slots, the group takes
+//    one pass over each half's keys, the other half's waves idle through it.
 //  * Keys stream in 64-row blocks. K goes to LDS as rows ([key][d], 16-byte chunks
 //    XOR-swizzled by key). V goes to LDS transposed ([d][key]) so the P*V operand is
 //    one 16-byte read per lane: each lane octet loads an 8 keys x 8 d block,
@@ -29,7 +32,7 @@
 
 namespace {
 
-constexpr int kQT = 1;              // 16-query tiles per wave
+constexpr int kQT = 2;              // 16-query tiles per wave
 constexpr int kRows = 64 * kQT;     // query rows per group (4 waves)
 constexpr int kKeys = 64;   // keys per block (two 32-key MFMA steps of P V)
 
@@ -167,35 +170,32 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     constexpr int kC = kKeys * 16 / (256 * HG);  // 16-byte K (and V) loads per thread and block
     __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
     __shared__ __attribute__((aligned(16))) char svt[128 * kKeys * 2];  // V transposed (vt_at)
-    __shared__ uint32_t srange[2];
+    __shared__ uint32_t srange[kQT][2];     // key range of each 64-row half
+    __shared__ uint32_t smixed;             // the halves belong to different slots
     __shared__ uint32_t stab_s[kMaxPages];  // this group's page-table entries
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
     const uint32_t G = p.heads / p.kv_heads, h = blockIdx.y * HG + (wave >> 2), kvh = h / G;
-    const uint32_t qw = wave & 3;  // the wave's 16 rows within the group's 64
+    const uint32_t qw = wave & 3;  // the wave's 16 kQT rows within the group's kRows
     const uint32_t r0 = blockIdx.x * kRows;
-    const uint32_t slot = p.slots[r0];
+    const uint32_t half = qw * kQT / 4;  // the 64-row half of the group holding the wave's rows
 
-    // Key range of the whole group: [lo, hi].
-    if (t == 0) { srange[0] = 0xffffffffu; srange[1] = 0; }
+    // Key range of each 64-row half, and whether the halves share a slot.
+    if (t < kQT) { srange[t][0] = 0xffffffffu; srange[t][1] = 0; }
+    if (t == 0) smixed = 0;
     __syncthreads();
     if (t < kRows && r0 + t < p.rows) {
         const uint32_t pos = p.positions[r0 + t];
-        atomicMin(&srange[0], pos > p.back ? pos - p.back : 0);
-        atomicMax(&srange[1], pos);
+        atomicMin(&srange[t / 64][0], pos > p.back ? pos - p.back : 0);
+        atomicMax(&srange[t / 64][1], pos);
+        if (p.slots[r0 + t] != p.slots[r0]) smixed = 1;
     }
     __syncthreads();
-    const uint32_t lo = srange[0] & ~(kKeys - 1), hi = srange[1];
-    // The page numbers of keys [lo, hi] into LDS once, so no key block waits on a
-    // dependent table load.
-    const uint32_t p0 = p.table ? lo >> p.page_shift : 0, np = p.table ? (hi >> p.page_shift) - p0 + 1 : 0;
-    const uint32_t *stab = nullptr;
-    if (p.table && np <= kMaxPages) {
-        for (uint32_t i = t; i < np; i += 256 * HG) stab_s[i] = p.table[(uint64_t)slot * p.kept_pages + p0 + i];
-        __syncthreads();
-        stab = stab_s;
-    }
+    // Rows come in 64-row blocks of one slot. Halves of one slot share every key
+    // block (one pass); halves of two slots take a pass each, the other half's waves
+    // idle through it with no live rows.
+    const uint32_t npass = smixed ? kQT : 1;
 
     // This wave's queries: r0 + 16 kQT wave + 16 qt + col. The q operand
     // (B, columns = queries), loaded once: lane group g holds d 32 g + 8 j .. + 8 for
@@ -244,6 +244,32 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
         for (int d = 0; d < 8; d++) o[qt][d] = f32x4{0, 0, 0, 0};
 
+    for (uint32_t pass = 0; pass < npass; pass++) {
+    if (r0 + 64 * pass >= p.rows) break;
+    const uint32_t slot = p.slots[r0 + 64 * pass];
+    uint32_t lo = srange[pass][0], hi = srange[pass][1];
+    if (npass == 1) {
+#pragma unroll
+        for (int i = 1; i < kQT; i++) { lo = min(lo, srange[i][0]); hi = max(hi, srange[i][1]); }
+    }
+    lo &= ~(kKeys - 1);
+    bool act[kQT];  // rows of this pass
+#pragma unroll
+    for (int qt = 0; qt < kQT; qt++) act[qt] = rlive[qt] && (npass == 1 || half == pass);
+    bool any = false;
+#pragma unroll
+    for (int qt = 0; qt < kQT; qt++) any |= act[qt];
+    const bool wave_on = __builtin_amdgcn_ballot_w64(any) != 0;  // else: stage and wait only
+    // The page numbers of keys [lo, hi] into LDS once, so no key block waits on a
+    // dependent table load.
+    if (pass) __syncthreads();  // every wave is done with the previous pass's table
+    const uint32_t p0 = p.table ? lo >> p.page_shift : 0, np = p.table ? (hi >> p.page_shift) - p0 + 1 : 0;
+    const uint32_t *stab = nullptr;
+    if (p.table && np <= kMaxPages) {
+        for (uint32_t i = t; i < np; i += 256 * HG) stab_s[i] = p.table[(uint64_t)slot * p.kept_pages + p0 + i];
+        __syncthreads();
+        stab = stab_s;
+    }
     u32x4 kr[kC], vr[kC];
     fetch_kv(p, slot, kvh, lo, hi, stab, p0, kr, vr);
     for (uint32_t kb = lo; kb <= hi; kb += kKeys) {
@@ -265,6 +291,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         // waits for LDS only).
         if (kb + kKeys <= hi) fetch_kv(p, slot, kvh, kb + kKeys, hi, stab, p0, kr, vr);
         lds_barrier();
+        if (!wave_on) continue;
 
         // S^T for four 16-key tiles x the query tiles.
         f32x4 s[4][kQT];
@@ -291,7 +318,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         // A block wholly inside every query's window of the wave skips the masks.
         bool inside = true;
 #pragma unroll
-        for (int qt = 0; qt < kQT; qt++) inside &= !rlive[qt] || (kb + kKeys - 1 <= rpos[qt] && kb >= rfrom[qt]);
+        for (int qt = 0; qt < kQT; qt++) inside &= !act[qt] || (kb + kKeys - 1 <= rpos[qt] && kb >= rfrom[qt]);
         inside = __builtin_amdgcn_ballot_w64(!inside) == 0;  // uniform
         bf16x8 ph[2][kQT], pl[2][kQT];
 #pragma unroll
@@ -304,7 +331,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int k = kt * 16 + 4 * (int)grp + i;
-                    const bool ok = inside || (rlive[qt] && k <= hi_off && k >= lo_off);
+                    const bool ok = inside || (act[qt] && k <= hi_off && k >= lo_off);
                     sv[kt][i] = ok ? s[kt][qt][i] * sl : -INFINITY;
                     mx = fmaxf(mx, sv[kt][i]);
                 }
@@ -364,6 +391,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             }
         }
     }
+
+    }  // pass
 
     // O / l: lane (query col of tile qt) holds d = 16 dt + 4 grp + i.
 #pragma unroll

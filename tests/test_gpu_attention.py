@@ -85,7 +85,7 @@ def test_decode_many_rows_per_slot():
     np.testing.assert_allclose(run("attend", c, 0.3), want(c, 0.3), atol=ATOL, rtol=0)
 
 
-@pytest.mark.parametrize("lens", [[1], [64], [100], [130, 70], [2048]])
+@pytest.mark.parametrize("lens", [[1], [64], [100], [130, 70], [2048], [64, 64, 64], [10, 64, 5]])
 def test_prefill_flash_rows(lens):
     """Prefill: each slot's rows at positions 0..len-1, slots padded to 64-row blocks
     apart (a 64-row block never crosses a slot)."""
