@@ -16,11 +16,11 @@
 //  * Rows come in 64-row blocks of one slot (the prefill shape: runs of one slot).
 //    When the group's two 64-row halves belong to different slots, the group takes
 //    one pass over each half's keys, the other half's waves idle through it.
-//  * Keys stream in 64-row blocks. K goes to LDS as rows ([key][d], 16-byte chunks
-//    XOR-swizzled by key). V goes to LDS transposed ([d][key]) so the P*V operand is
-//    one 16-byte read per lane: each lane octet loads an 8 keys x 8 d block,
-//    transposes it across the octet with lane shuffles and writes 16 bytes per lane
-//    (16-bit scattered writes bank-conflicted 16 ways and cost more than the MFMAs).
+//  * Keys stream in 64-row blocks. K and V go to LDS as rows ([key][d], 16-byte
+//    chunks XOR-swizzled by key), 16 bytes per lane, no reshuffling: the V^T operand
+//    of O^T += V^T P^T comes out of LDS already transposed through gfx950's
+//    ds_read_b64_tr_b16 (a lane octet transpose on the VALU cost more than the
+//    softmax before this).
 //  * The group's page-table entries are copied to LDS once.
 //  * S^T = K Q^T: 4 key tiles x 4 d-steps of v_mfma_f32_16x16x32_bf16 per q part
 //    (bf16 q as is; f32 q split into two exact bf16 parts). Online softmax per query
@@ -62,10 +62,8 @@ TS_DEV uint64_t key_row(const FlashParams &p, uint32_t slot, uint32_t pos, const
 
 // K and V of one 64-key block in flight, 16 bytes (8 d values) per load, kC loads per
 // thread (1024 / kC threads). K: thread t holds key idx / 16, chunk idx % 16
-// (idx = t + 1024 / kC c). V: wave w's load c covers keys
-// 8 kg + (l & 7) and chunks 8 cg + (l >> 3), g = kC w + c, kg = g & 7, cg = g >> 3, so
-// each lane octet holds an 8 keys x 8 d block for the octet transpose. Keys past the
-// last row's position may sit in pages never written: they load as zeros.
+// (idx = t + 1024 / kC c); V likewise. Keys past the last row's position may sit in
+// pages never written: they load as zeros.
 template <int kC>
 TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t kb, uint32_t hi, const uint32_t *stab,
                      uint32_t p0, u32x4 (&kr)[kC], u32x4 (&vr)[kC]) {
@@ -78,61 +76,12 @@ TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t
             const uint64_t row = key_row(p, slot, pos, stab, p0);
             kr[c] = *(const u32x4 *)(p.k + (row * p.kv_heads + kvh) * 128 + chunk * 8);
         }
-        const uint32_t g = kC * wave + c, vkey = 8 * (g & 7) + (lane & 7), vchunk = 8 * (g >> 3) + (lane >> 3);
-        const uint32_t vpos = kb + vkey;
         vr[c] = u32x4{0, 0, 0, 0};
-        if (vpos <= hi && (p.table || vpos < p.keys)) {
-            const uint64_t row = key_row(p, slot, vpos, stab, p0);
-            vr[c] = *(const u32x4 *)(p.v + (row * p.kv_heads + kvh) * 128 + vchunk * 8);
+        if (pos <= hi && (p.table || pos < p.keys)) {
+            const uint64_t row = key_row(p, slot, pos, stab, p0);
+            vr[c] = *(const u32x4 *)(p.v + (row * p.kv_heads + kvh) * 128 + chunk * 8);
         }
     }
-}
-
-// Lane exchanges within octets / quads on the VALU (DPP), not LDS permutes.
-TS_DEV uint32_t xor1(uint32_t x) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false); }
-TS_DEV uint32_t xor2(uint32_t x) { return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false); }
-// lane j of an octet takes lane j ^ 4: the octet mirrored (j -> 7 - j), then the
-// quad reversed (j -> j ^ 3).
-TS_DEV uint32_t xor4(uint32_t x) {
-    const int m = __builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);
-}
-
-// 8 x 8 transpose of bf16 across the 8 lanes of an octet: lane j holds row j (8 values
-// in 4 words) in, column j out. Three butterfly stages swap the off-diagonal blocks
-// between lanes j and j ^ 4, j ^ 2, j ^ 1.
-TS_DEV u32x4 transpose8(u32x4 v, uint32_t j) {
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-    {  // lanes ^ 4: words {2, 3} of the low lane <-> words {0, 1} of the high lane
-        const bool up = j & 4;
-        const uint32_t s0 = up ? w[0] : w[2], s1 = up ? w[1] : w[3];
-        const uint32_t r0 = xor4(s0), r1 = xor4(s1);
-        if (up) { w[0] = r0; w[1] = r1; } else { w[2] = r0; w[3] = r1; }
-    }
-    {  // lanes ^ 2: words {1, 3} of the low lane <-> words {0, 2} of the high lane
-        const bool up = j & 2;
-        const uint32_t s0 = up ? w[0] : w[1], s1 = up ? w[2] : w[3];
-        const uint32_t r0 = xor2(s0), r1 = xor2(s1);
-        if (up) { w[0] = r0; w[2] = r1; } else { w[1] = r0; w[3] = r1; }
-    }
-    {  // lanes ^ 1: the high halves of the low lane <-> the low halves of the high lane
-        const bool up = j & 1;
-        const uint32_t s0 = up ? (w[0] & 0xffffu) | (w[1] << 16) : (w[0] >> 16) | (w[1] & 0xffff0000u);
-        const uint32_t s1 = up ? (w[2] & 0xffffu) | (w[3] << 16) : (w[2] >> 16) | (w[3] & 0xffff0000u);
-        const uint32_t r0 = xor1(s0), r1 = xor1(s1);
-        if (up) {
-            w[0] = (w[0] & 0xffff0000u) | (r0 & 0xffffu);
-            w[1] = (w[1] & 0xffff0000u) | (r0 >> 16);
-            w[2] = (w[2] & 0xffff0000u) | (r1 & 0xffffu);
-            w[3] = (w[3] & 0xffff0000u) | (r1 >> 16);
-        } else {
-            w[0] = (w[0] & 0xffffu) | (r0 << 16);
-            w[1] = (w[1] & 0xffffu) | (r0 & 0xffff0000u);
-            w[2] = (w[2] & 0xffffu) | (r1 << 16);
-            w[3] = (w[3] & 0xffffu) | (r1 & 0xffff0000u);
-        }
-    }
-    return u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // Sums and maxima over the four 16-lane rows of a wave, in every lane (gfx950
@@ -150,12 +99,19 @@ TS_DEV float rows4_max(float x) {
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-// V^T in LDS: row d holds the block's 64 keys in the order the P^T operands use:
-// key 32 s + 16 t + 4 g + i (step s, tile t, group g, i < 4) at position
-// 32 s + 8 g + 4 t + i, so lane group g reads its 8 keys of step s as one 16-byte
-// chunk. Chunks XOR-swizzled by d % 8 so 8 consecutive d rows hit distinct banks.
-// Byte offset of position q (a multiple of 4).
-TS_DEV uint32_t vt_at(uint32_t d, uint32_t q) { return d * 128 + (((q >> 3) ^ (d & 7)) << 4) + (q & 7) * 2; }
+// V^T operand straight from row-major V with gfx950's transposing LDS read
+// (ds_read_b64_tr_b16): within each 16-lane block, lane i receives element i % 4 of
+// the 8-byte pieces addressed by lanes i / 4 + 4 e, e = 0..3. Lane L = 4 e + c of
+// block g addresses key k0 + e, d = d0 + 4 c, so lane i ends with d0 + i of keys
+// k0 .. k0 + 3: four consecutive keys of one d, as the MFMA A operand wants.
+typedef short ts_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) ts_v4i16 lds_v4i16;
+TS_DEV u32x2 read_vt4(const uint16_t (*sv)[128], uint32_t key, uint32_t d) {
+    const uint32_t chunk = d >> 3;
+    const uint16_t *a = &sv[key][((chunk ^ (key & 15)) << 3) + (d & 7)];
+    const ts_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)a);
+    return __builtin_bit_cast(u32x2, v);
+}
 
 // The transposed formulation: S^T = K Q^T and O^T = V^T P^T. With K as the A
 // operand (rows = keys) and Q^T as B (columns = queries), the S^T accumulator lane
@@ -169,7 +125,7 @@ template <bool QF32, int HG>
 __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     constexpr int kC = kKeys * 16 / (256 * HG);  // 16-byte K (and V) loads per thread and block
     __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
-    __shared__ __attribute__((aligned(16))) char svt[128 * kKeys * 2];  // V transposed (vt_at)
+    __shared__ __attribute__((aligned(16))) uint16_t sv[kKeys][128];     // V rows, swizzled as K
     __shared__ uint32_t srange[kQT][2];     // key range of each 64-row half
     __shared__ uint32_t smixed;             // the halves belong to different slots
     __shared__ uint32_t stab_s[kMaxPages];  // this group's page-table entries
@@ -279,13 +235,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         for (int c = 0; c < kC; c++) {
             const uint32_t idx = t + 256 * HG * c, key = idx >> 4, chunk = idx & 15;
             *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c];
-            // V: after the octet transpose lane j holds d = 8 vchunk + j for keys
-            // 8 kg .. 8 kg + 7 (step kg / 4), at positions q0 .. q0 + 3 and q0 + 8 .. + 11.
-            const uint32_t g = kC * wave + c, kg = g & 7, vchunk = 8 * (g >> 3) + (lane >> 3), ks = kg & 3;
-            const uint32_t d = vchunk * 8 + (lane & 7), q0 = 32 * (kg >> 2) + 16 * (ks & 1) + 4 * (ks >> 1);
-            const u32x4 tv = transpose8(vr[c], lane & 7);
-            *(u32x2 *)(svt + vt_at(d, q0)) = u32x2{tv.x, tv.y};
-            *(u32x2 *)(svt + vt_at(d, q0 + 8)) = u32x2{tv.z, tv.w};
+            *(u32x4 *)&sv[key][(chunk ^ (key & 15)) * 8] = vr[c];
         }
         // The next block's loads fly while this one computes (the barrier below
         // waits for LDS only).
@@ -382,7 +332,11 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         for (int d = 0; d < 8; d++) {
 #pragma unroll
             for (int st = 0; st < 2; st++) {
-                const bf16x8 vf = as_bf16x8(*(const u32x4 *)(svt + vt_at(d * 16 + col, 32 * st + 8 * grp)));
+                // Positions 8 grp .. + 3 and + 4 .. + 7 of step st hold keys
+                // 32 st + 4 grp + i and 32 st + 16 + 4 grp + i (P^T's order).
+                const uint32_t key = 32 * st + 4 * grp + (col >> 2), dd = d * 16 + 4 * (col & 3);
+                const u32x2 va = read_vt4(sv, key, dd), vb = read_vt4(sv, key + 16, dd);
+                const bf16x8 vf = as_bf16x8(u32x4{va.x, va.y, vb.x, vb.y});
 #pragma unroll
                 for (int qt = 0; qt < kQT; qt++) {
                     o[qt][d] = mfma16(vf, ph[st][qt], o[qt][d]);
