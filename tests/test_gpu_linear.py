@@ -63,10 +63,13 @@ def test_linear_bf16_sweep_shapes(m, k, n):
 
 
 @pytest.mark.parametrize("m,n,k", [(2048, 8192, 256), (2000, 7777, 192), (2000, 7777, 136), (1300, 12300, 64),
-                                   (4096, 16384, 128)])
+                                   (4096, 16384, 128), (2048, 20000, 1024)])
 def test_tiled_256_tiles(m, n, k):
-    """Products with enough 256x256 tiles take the big-tile kernel (bf16 x and w): one
-    tile per CU, ragged edges, several tiles per CU (4096 x 16384)."""
+    """Products with enough 256x256 tiles take the big-tile kernel (bf16 x and w, k a
+    multiple of 64): one tile per CU, ragged edges, several tiles per CU (4096 x 16384;
+    2048 x 20000 mixes whole tiles with a ragged last column of tiles); k 136 takes
+    the 128x128 kernel. Each product runs with an added operand, to f32 and to
+    bf16."""
     R = _rules()
     O.set_threads(O.lib().or_threads_available())
     r = rng(m + n + k)
@@ -77,6 +80,8 @@ def test_tiled_256_tiles(m, n, k):
     res = r.standard_normal((m, n)).astype(np.float32)
     got = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), a0=to_dev(res, torch)))
     _check(got, want + res, _bound(xf, wf) + 1e-5)
+    got32 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch)))
+    _check(got32, want, _bound(xf, wf))
     got16 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), out_dtype=torch.bfloat16))
     assert max_rel(got16, want) <= 2e-2
 
