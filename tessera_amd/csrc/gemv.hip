@@ -312,19 +312,30 @@ void gemv_plan(uint32_t n, uint32_t k, bool silu, bool w8, int *rows, uint32_t *
             return;
         }
     }
-    // Measured on MI355X (graph-replayed, cold weights): one wave per group is
-    // fastest at every decode shape (an LDS exchange costs more than it saves),
-    // and rows per wave grow with the row count: 8 for >= 3072 rows of 1024,
+    // Measured on MI355X (graph-replayed, cold weights): for bf16 weights one wave
+    // per group is fastest at every decode shape (an LDS exchange costs more than it
+    // saves), and rows per wave grow with the row count: 8 for >= 3072 rows of 1024,
     // 4 for ~1024 rows of 2048, 2 for ~1024 rows of 3072.
-    (void)w8;
     const uint32_t total = silu ? 2 * n : n;
     int r;
-    if (total >= 3072) r = 8;
-    else if (k <= 2048) r = 4;
-    else r = 2;
+    uint32_t w = 1;
+    if (w8) {
+        // e4m3 rows (16 weights per 16-byte load): measured on the C4 shapes. Rows much
+        // longer than the row count leave too few waves with one wave per group, so four
+        // waves split k there (4096 x 14336: 20.3 -> 12.8 us at m = 1).
+        if (k >= 3 * total && total >= 4096) { r = 8; w = 4; }
+        else if (total >= 8192) r = 8;
+        else if (total >= 4096) r = 4;
+        else r = 2;
+    } else if (total >= 3072) {
+        r = 8;
+    } else if (k <= 2048) {
+        r = 4;
+    } else {
+        r = 2;
+    }
     const uint32_t outs = silu ? r / 2 : r;
     const uint32_t g = (n + outs - 1) / outs;
-    const uint32_t w = 1;
     *rows = r;
     *waves = w;
     *groups = g;
