@@ -60,14 +60,23 @@ __global__ __launch_bounds__(kScan) void route_scan(uint32_t *offs, uint32_t chu
     __shared__ uint32_t part[kScan], tpart[kScan];
     const uint32_t B = count + 1, t = threadIdx.x;
     const uint32_t per = (B + kScan - 1) / kScan, b0 = t * per, b1 = min(B, b0 + per);
-    // Totals of this thread's buckets (each bucket's chunk prefix in place).
+    // Totals of this thread's buckets (each bucket's chunk prefix in place). The
+    // counts are loaded 16 at a time before any is rewritten: a load after a store to
+    // the same array would otherwise wait for the store, one memory round trip per chunk.
+    constexpr uint32_t kBatch = 16;
     uint32_t seg = 0, tseg = 0;
     for (uint32_t b = b0; b < b1; b++) {
         uint32_t s = 0;
-        for (uint32_t c = 0; c < chunks; c++) {
-            const uint32_t v = offs[(size_t)c * B + b];
-            offs[(size_t)c * B + b] = s;
-            s += v;
+        for (uint32_t c0 = 0; c0 < chunks; c0 += kBatch) {
+            uint32_t v[kBatch];
+#pragma unroll
+            for (uint32_t i = 0; i < kBatch; i++) v[i] = c0 + i < chunks ? offs[(size_t)(c0 + i) * B + b] : 0u;
+#pragma unroll
+            for (uint32_t i = 0; i < kBatch; i++)
+                if (c0 + i < chunks) {
+                    offs[(size_t)(c0 + i) * B + b] = s;
+                    s += v[i];
+                }
         }
         row_start[b] = s;  // total for now
         seg += s;
@@ -81,7 +90,14 @@ __global__ __launch_bounds__(kScan) void route_scan(uint32_t *offs, uint32_t chu
     for (uint32_t b = b0; b < b1; b++) {
         const uint32_t tot = row_start[b];
         row_start[b] = base;
-        for (uint32_t c = 0; c < chunks; c++) offs[(size_t)c * B + b] += base;
+        for (uint32_t c0 = 0; c0 < chunks; c0 += kBatch) {
+            uint32_t v[kBatch];
+#pragma unroll
+            for (uint32_t i = 0; i < kBatch; i++) v[i] = c0 + i < chunks ? offs[(size_t)(c0 + i) * B + b] : 0u;
+#pragma unroll
+            for (uint32_t i = 0; i < kBatch; i++)
+                if (c0 + i < chunks) offs[(size_t)(c0 + i) * B + b] = v[i] + base;
+        }
         if (b < count) {
             tile_start[b] = tbase;
             tbase += (tot + tile_rows - 1) / tile_rows;
