@@ -140,11 +140,45 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_big_kernel(BigParams p) {
     }
     mfma_step<false>(p, lds, steps - 1, acc, m0, n0, wave, lane, wm, wn, col, grp);
 
-    // Epilogue. The MFMA operands are swapped (weights first), so lane l holds row
-    // col of each 16x16 tile and its four adjacent columns 4 grp .. + 3: one 8-byte
-    // (bf16) or 16-byte (f32) store per lane and tile instead of four 2-byte ones
-    // (the scattered stores took a fifth of the lm_head product's time).
     const uint32_t N = p.n, M = p.m;
+    if (p.out_bf16 && !(p.stages & TS_AFTER_ADD)) {
+        // bf16 output with no added operand: the tile goes through LDS (the stages
+        // are free once every wave has read the last one) as 256 rows of 512 B,
+        // 16-byte chunks XOR-swizzled by row, and leaves as whole rows: two rows of
+        // 512 contiguous bytes per store instruction instead of 16 rows x 32 B.
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t r = wm * 128 + i * 16 + col;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t c = wn * 64 + j * 16 + 4 * grp;  // first of 4 columns (8 B)
+                const f32x4 v = acc[i][j];
+                *(u32x2 *)(lds + r * 512 + ((((c >> 3) ^ (r & 31))) << 4) + (c & 7) * 2) =
+                    u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            }
+        }
+        lds_barrier();
+        const bool rows16 = (N & 7) == 0;  // every row starts 16-byte aligned
+#pragma unroll 4
+        for (int it = 0; it < 16; it++) {
+            const uint32_t f = it * kThreads + t, r = f >> 5, c = f & 31;
+            const uint32_t m = m0 + r, n = n0 + c * 8;
+            if (m >= M || n >= N) continue;
+            const u32x4 v = *(const u32x4 *)(lds + r * 512 + ((c ^ (r & 31)) << 4));
+            uint16_t *o = (uint16_t *)p.out + (size_t)m * N + n;
+            if (rows16 && n + 8 <= N) {
+                *(u32x4 *)o = v;
+            } else {
+                for (uint32_t e = 0; e < 8 && n + e < N; e++) o[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+            }
+        }
+        return;
+    }
+    // Epilogue with f32 output or an added operand. The MFMA operands are swapped
+    // (weights first), so lane l holds row col of each 16x16 tile and its four
+    // adjacent columns 4 grp .. + 3: one 8-byte (bf16) or 16-byte (f32) store per
+    // lane and tile instead of four 2-byte ones.
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const uint32_t m = m0 + wm * 128 + i * 16 + col;

@@ -84,6 +84,9 @@ def test_tiled_256_tiles(m, n, k):
     _check(got32, want, _bound(xf, wf))
     got16 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), out_dtype=torch.bfloat16))
     assert max_rel(got16, want) <= 2e-2
+    # Same sums, one rounding: the bf16 output is the f32 output rounded to nearest
+    # even, element for element (pins where each value lands in the bf16 epilogue).
+    assert np.array_equal(got16, O.bf16_widen(O.bf16_narrow(got32)))
 
 
 def test_lanes_and_tiled_agree_at_16_rows():
