@@ -53,6 +53,8 @@ def parse():
                    help="run only the C3/C4/C5 measurements (for kernel traces of those rows)")
     p.add_argument("--decode-only", action="store_true",
                    help="only the decode measurement (and a 256 MiB copy: the PMC yardstick)")
+    p.add_argument("--gemm-only", action="store_true",
+                   help="run only the C2 sweep at M=2048 (for kernel traces and PMC passes of tiled)")
     p.add_argument("--roofline-only", action="store_true",
                    help="run only the lm_head lanes kernel and a plain copy of known size "
                         "(the rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes)")
@@ -325,6 +327,9 @@ def main():
         roof = lm_head_roofline(torch, reps=5)
         copy_reference(torch)
         print(json.dumps({"roofline": roof}), flush=True)
+        return
+    if a.gemm_only:
+        print(json.dumps({"prefill_gemm": gemm_sweep(torch)}), flush=True)
         return
     if a.rows_only:
         print(json.dumps({"c3_decode": c3_decode(torch), "c3_prefill": c3_prefill(torch), "c4_fp8": c4(torch),

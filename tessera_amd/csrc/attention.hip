@@ -566,14 +566,35 @@ __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t 
     const float *all = p.partials + gi * parts * G * 130;
     for (uint32_t e = threadIdx.x; e < G * 128; e += blockDim.x) {
         const uint32_t h = e / 128, d = e % 128;
+        // Partitions in batches of 8 with every load of a batch issued before use
+        // (clamped indices are read, not used); sums stay in partition order.
+        constexpr uint32_t kB = 8;
         float M = -INFINITY;
-        for (uint32_t q = 0; q < parts; q++) M = fmaxf(M, all[(q * G + h) * 130]);
+        for (uint32_t q0 = 0; q0 < parts; q0 += kB) {
+            float mq[kB];
+#pragma unroll
+            for (uint32_t j = 0; j < kB; j++) mq[j] = all[(min(q0 + j, parts - 1) * G + h) * 130];
+#pragma unroll
+            for (uint32_t j = 0; j < kB; j++)
+                if (q0 + j < parts) M = fmaxf(M, mq[j]);
+        }
         float L = 0.0f, O = 0.0f;
-        for (uint32_t q = 0; q < parts; q++) {
-            const float *pq = all + (q * G + h) * 130;
-            const float f = (pq[0] == -INFINITY) ? 0.0f : expf(pq[0] - M);
-            L += pq[1] * f;
-            O += pq[2 + d] * f;
+        for (uint32_t q0 = 0; q0 < parts; q0 += kB) {
+            float mq[kB], lq[kB], oq[kB];
+#pragma unroll
+            for (uint32_t j = 0; j < kB; j++) {
+                const float *pq = all + (min(q0 + j, parts - 1) * G + h) * 130;
+                mq[j] = pq[0];
+                lq[j] = pq[1];
+                oq[j] = pq[2 + d];
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kB; j++)
+                if (q0 + j < parts) {
+                    const float f = (mq[j] == -INFINITY) ? 0.0f : expf(mq[j] - M);
+                    L += lq[j] * f;
+                    O += oq[j] * f;
+                }
         }
         p.out[((size_t)r * p.heads + kvh * G + h) * 128 + d] = O / L;
     }

@@ -317,10 +317,25 @@ __global__ __launch_bounds__(256) void lanes_finish(LanesParams p, const float *
     const uint64_t i = blockIdx.x * 256ull + threadIdx.x, MN = (uint64_t)p.m * p.n;
     if (i >= MN) return;
     const uint32_t n = (uint32_t)(i % p.n), N = p.n;
+    // Eight splits' loads in flight at a time, added in split order (the same sums
+    // as one split at a time).
+    constexpr uint32_t kB = 8;
+    const size_t stride = (size_t)(SILU ? 2 : 1) * MN;
     float g = 0.0f, u = 0.0f;
-    for (uint32_t s = 0; s < splits; s++) {
-        g += part[(size_t)s * (SILU ? 2 : 1) * MN + i];
-        if (SILU) u += part[(size_t)s * 2 * MN + MN + i];
+    for (uint32_t s0 = 0; s0 < splits; s0 += kB) {
+        float tg[kB], tu[kB];
+#pragma unroll
+        for (uint32_t j = 0; j < kB; j++) {
+            const uint32_t s = min(s0 + j, splits - 1);  // clamped: read but not added
+            tg[j] = part[s * stride + i];
+            if (SILU) tu[j] = part[s * stride + MN + i];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kB; j++)
+            if (s0 + j < splits) {
+                g += tg[j];
+                if (SILU) u += tu[j];
+            }
     }
     if (W8) {
         g *= bf16_float(p.w_scale[n]);
@@ -337,12 +352,13 @@ struct Plan {
 };
 
 // Enough groups to cover the chip (~512): the column groups, times a k split when
-// they are fewer (each split keeps at least one 128-deep chunk).
+// they are fewer. Each split keeps at least two 128-deep chunks: one-chunk splits
+// measured slower (4096 x 1024 e4m3 at m 8: 7.0 us against 5.9 us with two).
 Plan plan(const ts_linear_args *a) {
     Plan pl;
     const uint32_t tiles = (a->n + 15) / 16, chunks = (a->k + kChunk - 1) / kChunk;
     pl.groups = (tiles + kWaves - 1) / kWaves;
-    pl.splits = std::max(1u, std::min(chunks, (512u + pl.groups - 1) / pl.groups));
+    pl.splits = std::max(1u, std::min(chunks / 2, (512u + pl.groups - 1) / pl.groups));
     return pl;
 }
 

@@ -381,12 +381,13 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
 
 extern "C" void tessera_qwen3_close(ts_qwen3 *m) {
     if (!m) return;
-    if (m->stream) hipStreamSynchronize(m->stream);
-    if (m->graph) hipGraphExecDestroy(m->graph);
-    for (void *p : m->allocs) hipFree(p);
+    // Teardown: errors here have no caller to report to; every resource is released regardless.
+    if (m->stream) (void)hipStreamSynchronize(m->stream);
+    if (m->graph) (void)hipGraphExecDestroy(m->graph);
+    for (void *p : m->allocs) (void)hipFree(p);
     if (m->ev0) (void)hipEventDestroy(m->ev0);
     if (m->ev1) (void)hipEventDestroy(m->ev1);
-    if (m->stream) hipStreamDestroy(m->stream);
+    if (m->stream) (void)hipStreamDestroy(m->stream);
     if (m->pool) tessera_kv_free(m->pool);
     delete m;
 }
@@ -480,12 +481,12 @@ extern "C" int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *token
         int rc = decode_step(m);
         e = hipStreamEndCapture(m->stream, &g);
         if (rc != TS_OK) {
-            if (g) hipGraphDestroy(g);
+            if (g) (void)hipGraphDestroy(g);
             return rc;
         }
         if (e != hipSuccess) return ts::hip_status(e, "hipStreamEndCapture");
         e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         if (e != hipSuccess) return ts::hip_status(e, "hipGraphInstantiate");
     }
     for (uint32_t i = 0; i < steps && !m->use_step; i++) {

@@ -56,8 +56,8 @@ def test_workspace_sizes():
     a.m, a.n, a.k = 1, 1024, 3072
     assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 0  # m <= 4: the vector-ALU kernel, no split
     a.m, a.n, a.k = 64, 1024, 4096
-    # 16 column groups of 64; k split 32 ways (one 128-deep chunk each): raw f32 sums
-    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 32 * 64 * 1024 * 4
+    # 16 column groups of 64; k split 16 ways (two 128-deep chunks each): raw f32 sums
+    assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 16 * 64 * 1024 * 4
     a.m, a.n, a.k = 8, 14336, 4096
     assert lib.tessera_hip_lanes_workspace(C.byref(a)) == 3 * 8 * 14336 * 4
     r = abi.RowsArgs()
