@@ -649,15 +649,22 @@ int check(const ts_rows_args *a) {
     return TS_OK;
 }
 
-}  // namespace
-
-extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
-    if (!a || a->kv_heads == 0) return 0;
-    Split s = split(a, false);
+// Bytes of split-KV partials a launch with split s writes: [rows][kv_heads][parts][G][130].
+size_t partials_bytes(const ts_rows_args *a, const Split &s) {
     if (s.parts <= 1) return 0;
     const size_t G = a->heads / a->kv_heads;
     const size_t groups = (size_t)a->rows * a->kv_heads;
     return groups * s.parts * G * 130 * sizeof(float);
+}
+
+}  // namespace
+
+// One size serves both entry points (tessera_hip_attend_rows and the fused
+// tessera_hip_attend_step split the same span differently past 2048 keys): the
+// larger of the two.
+extern "C" size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a) {
+    if (!a || a->kv_heads == 0 || a->heads % a->kv_heads) return 0;
+    return std::max(partials_bytes(a, split(a, false)), partials_bytes(a, split(a, true)));
 }
 
 namespace {
@@ -681,7 +688,7 @@ int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     p.marks = ts_debug_marks();
 #endif
     if (s.parts > 1) {
-        const size_t need = tessera_hip_attend_rows_workspace(a);
+        const size_t need = partials_bytes(a, s);  // what this launch writes
         if (!a->workspace || a->workspace_bytes < need)
             return ts::fail(TS_ERR_WORKSPACE, "attend_rows: workspace of %zu bytes needed", need);
         p.partials = (float *)a->workspace;

@@ -65,8 +65,29 @@ def test_workspace_sizes():
     r.max_position = 150
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 0  # one group per (row, kv head)
     r.max_position = 8191
-    # long context: 8 waves x 8 iterations x 32 keys per group, 4 partitions of
-    # (max, sum, 128 acc) per (row, kv head, head)
-    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 4 * 2 * 130 * 4
+    # long context: attend_rows streams 8 waves x 8 iterations x 32 keys per group (4
+    # partitions of (max, sum, 128 acc) per (row, kv head, head)), but the fused
+    # attend_step splits the same span into groups of 8 waves x 32 keys (32
+    # partitions); the one size covers both
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 32 * 2 * 130 * 4
+    r.rows, r.max_position = 1, 2999  # test_attend_step_fused's ctx 3000: 6 and 12 partitions
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 1 * 8 * 12 * 2 * 130 * 4
+    r.rows = 32
     r.max_position = 2047  # the short-context kernel: 8 waves x 32 keys, 8 partitions
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 8 * 2 * 130 * 4
+
+
+def test_attend_step_refuses_workspace_sized_for_attend_rows():
+    """Past 2048 keys the fused step splits a span into more partitions than
+    attend_rows does; a workspace that holds only attend_rows' partials is refused
+    with TS_ERR_WORKSPACE before anything launches (fake device addresses suffice)."""
+    lib = abi.load()
+    r = abi.RowsArgs()
+    fake = 1 << 20  # 16-byte aligned, never dereferenced on this path
+    r.q = r.k = r.v = r.out = r.slots = r.positions = r.kept_table = r.workspace = fake
+    r.rows, r.heads, r.kv_heads, r.width, r.page, r.kept_pages = 1, 16, 8, 128, 16, 188
+    r.scale, r.q_dtype, r.kv_dtype, r.out_dtype = 0.088, abi.TS_F32, abi.TS_BF16, abi.TS_F32
+    r.max_position = 2999
+    r.workspace_bytes = 1 * 8 * 6 * 2 * 130 * 4  # attend_rows' 6 partitions at this span
+    rc = lib.tessera_hip_attend_step(C.byref(r), fake, fake, fake, fake, 3000, C.c_float(1e-6), None)
+    assert rc == abi.TS_ERR_WORKSPACE
