@@ -248,6 +248,34 @@ def c4(torch):
     return {"bound": "hbm", "shapes": res, "aggregate_frac": round(bytes_all / t_all / HBM_PEAK, 4)}
 
 
+def blocks(torch):
+    """Block-form weights on the m = 1 decode product (q8_0, mxfp8, int4_g32: 32 codes a
+    block under one scale): the Qwen3 lm_head (151936 x 1024) and the Llama-3-8B-like
+    gate (14336 x 4096) shapes, HBM-bound. Bytes = packed rows + 4K (x) + 4N (out)."""
+    from tessera_amd import rules
+    sizes = {"q8_0": 34, "mxfp8": 33, "int4_g32": 18}
+    res, bytes_all, t_all = {}, 0.0, 0.0
+    for shape, (K, N) in {"lm_head": (1024, 151936), "gate": (4096, 14336)}.items():
+        x = torch.randn((1, K), device="cuda")
+        for form, bb in sizes.items():
+            rb = K // 32 * bb
+            w = torch.randint(0, 256, (N, rb), device="cuda", dtype=torch.uint8)
+            if form != "mxfp8":  # finite f16 scales
+                w.view(N, K // 32, bb)[:, :, 1] = 0x20
+            else:
+                w.view(N, K // 32, bb)[:, :, 0] = 120
+                w.view(N, K // 32, bb)[:, :, 1:] &= 0x77  # no NaN codes
+            out = torch.empty((1, N), device="cuda")
+            fn = lambda: rules.lanes(x, w, out=out, w_form=form)
+            t = _graph_time(torch, fn, launches=20)
+            nb = N * rb + 4 * K + 4 * N
+            res[f"{shape}_{form}"] = {"us": round(t * 1e6, 2), "frac": round(nb / t / HBM_PEAK, 4)}
+            bytes_all += nb
+            t_all += t
+            del w
+    return {"bound": "hbm", "shapes": res, "aggregate_frac": round(bytes_all / t_all / HBM_PEAK, 4)}
+
+
 def c5(torch):
     """C5: one MoE layer, 4096 tokens, hidden 4096, 128 experts top-8 (softmax over the
     8 picked logits), FFN 1536, plus one shared expert; gate logits N(0,1) f32 (seed 3).
@@ -333,7 +361,7 @@ def main():
         return
     if a.rows_only:
         print(json.dumps({"c3_decode": c3_decode(torch), "c3_prefill": c3_prefill(torch), "c4_fp8": c4(torch),
-                          "c5_moe": c5(torch)}), flush=True)
+                          "c5_moe": c5(torch), "block_forms": blocks(torch)}), flush=True)
         return
     from tessera_amd.qwen3 import Qwen3, default_config
     cfg = default_config(max_context=PROMPT + max(a.steps, a.warmup) + 1, max_prompt=PROMPT)
@@ -375,6 +403,7 @@ def main():
         extra["c3_prefill"] = c3_prefill(torch)
         extra["c4_fp8"] = c4(torch)
         extra["c5_moe"] = c5(torch)
+        extra["block_forms"] = blocks(torch)
     line = {
         "metric": "decode tok/s + % HBM roofline (Qwen3-0.6B-shape b=1); prefill GEMM % MFMA peak",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,

@@ -33,8 +33,14 @@ extern "C" {
 #define TS_ERR_ARCH (-2)      /* the current device is not gfx950 */
 #define TS_ERR_WORKSPACE (-3) /* workspace missing or too small */
 
-/* Storage types (engine/ir/mem/src/form.rs forms used on this path). */
-enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3 };
+/* Storage types (engine/ir/mem/src/form.rs forms used on this path). The block forms
+ * (engine/ir/mem/src/block.rs:258-286) hold each weight row as k/32 blocks, each one
+ * scale then 32 codes, rows back to back (k a multiple of 128); w_scale is unused:
+ *   TS_Q8_0      34 B a block: f16 scale, 32 signed bytes
+ *   TS_MXFP8     33 B a block: e8m0 scale, 32 e4m3 codes
+ *   TS_INT4_G32  18 B a block: f16 scale, 32 nibbles (code - 8), low nibble first
+ * They are accepted by tessera_hip_lanes / tessera_hip_linear for m <= 4 rows. */
+enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 = 5, TS_INT4_G32 = 6 };
 
 /* Fused stages around a product (engine/plan/lower/src/kernels/map.rs:20-59 MapStage,
  * applied by `finish` at the store, map.rs:155-185). */
@@ -84,7 +90,8 @@ int tessera_hip_linear(const ts_linear_args *a, void *stream);
 size_t tessera_hip_linear_workspace(const ts_linear_args *a);
 
 /* Few rows (m <= 64): m <= 4 on the vector ALU (a wave streams whole weight
- * rows); 5..64 on the matrix unit: a wave per 16 output columns, x staged once
+ * rows; block-form weights decode there too, bit-identical to the reference's
+ * Block::dot, engine/ir/mem/src/block.rs:202-219); 5..64 on the matrix unit: a wave per 16 output columns, x staged once
  * per group in LDS, weights streamed once with 64-byte runs per lane, k split
  * across groups when the columns alone do not cover the chip (partials in the
  * workspace, summed in split order by a second kernel: deterministic).

@@ -74,6 +74,15 @@ def lib():
         "or_take": (None, [_f32p, _i64, _i64, _u32p, _i64, _f32p]),
         "or_gather": (None, [C.c_void_p, _i64, _i64, _u32p, _i64, _i64, C.c_void_p]),
         "or_mix": (None, [_f32p, _i64, _i64, _i64, C.c_void_p, _f32p]),
+        "or_f16_narrow": (C.c_uint16, [C.c_float]),
+        "or_f16_widen": (C.c_float, [C.c_uint16]),
+        "or_e8m0_narrow": (C.c_uint8, [C.c_float]),
+        "or_e8m0_widen": (C.c_float, [C.c_uint8]),
+        "or_block_bytes": (C.c_int, [C.c_int]),
+        "or_block_pack": (None, [C.c_int, _f32p, _i64, _u8p]),
+        "or_block_unpack": (C.c_float, [C.c_int, _u8p, _i64]),
+        "or_block_dot": (C.c_float, [C.c_int, _f32p, _u8p, _i64]),
+        "or_block_product": (None, [C.c_int, _i64, _i64, _i64, _f32p, _u8p, _f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -322,4 +331,47 @@ def mix(x, weights=None) -> np.ndarray:
         weights = _f32(weights)
         wp = weights.ctypes.data
     lib().or_mix(x.reshape(-1), outer, count, inner, wp, out.reshape(-1))
+    return out
+
+
+# --- block forms: engine/ir/mem/src/block.rs:1-291 --------------------------------
+# Each form: 32 codes after one scale per block, no head. Rows of a [n, k] matrix are
+# packed one after another (k a multiple of 32, so blocks never straddle rows).
+BLOCK_FORMS = {"q8_0": 0, "mxfp8": 1, "int4_g32": 2}
+
+
+def block_bytes(form: str) -> int:
+    return lib().or_block_bytes(BLOCK_FORMS[form])
+
+
+def block_pack(form: str, w) -> np.ndarray:
+    """Packs each row of w [n, k] (k % 32 == 0) into [n, k / 32 * block_bytes] bytes."""
+    w = _f32(np.atleast_2d(w))
+    n, k = w.shape
+    assert k % 32 == 0
+    rb = k // 32 * block_bytes(form)
+    out = np.zeros((n, rb), np.uint8)
+    for r in range(n):
+        lib().or_block_pack(BLOCK_FORMS[form], w[r], k, out[r])
+    return out
+
+
+def block_unpack(form: str, bytes_row: np.ndarray, k: int) -> np.ndarray:
+    b = np.ascontiguousarray(bytes_row, dtype=np.uint8)
+    return np.array([lib().or_block_unpack(BLOCK_FORMS[form], b, i) for i in range(k)], np.float32)
+
+
+def block_dot(form: str, x, bytes_row) -> float:
+    x = _f32(x)
+    return lib().or_block_dot(BLOCK_FORMS[form], x, np.ascontiguousarray(bytes_row, dtype=np.uint8), x.size)
+
+
+def block_product(form: str, x, wb) -> np.ndarray:
+    """out[m, r] = dot(x[m], packed row r), the reference's Block::dot per output."""
+    x = _f32(np.atleast_2d(x))
+    wb = np.ascontiguousarray(wb, dtype=np.uint8)
+    m, k = x.shape
+    n = wb.shape[0]
+    out = np.empty((m, n), np.float32)
+    lib().or_block_product(BLOCK_FORMS[form], m, n, k, x, wb.reshape(-1), out)
     return out

@@ -20,6 +20,11 @@
  *   top_k                         brute-force stable sort
  *   gather, take, mix             gather_rows, closed forms
  *   paged row                     closed form of kept.rs Paged::row
+ *   f16, e8m0                     exhaustive f16 code round trips, numpy's RNE float16
+ *                                 on random f32, e8m0 round-up closed forms
+ *   block pack / dot              blocks_round_trip of block_test.rs (byte counts,
+ *                                 round-trip share, dot == sum over unpacked), hand-built
+ *                                 blocks with closed-form sums, code placement by form
  */
 #include <math.h>
 #include <stdint.h>
@@ -104,6 +109,137 @@ static inline float widen16(uint16_t b) {
 EXPORT float or_bf16_widen(uint16_t b) { return widen16(b); }
 EXPORT uint8_t or_e4m3_narrow(float x) { return (uint8_t)narrow_fmt(x, 4, 3, 0, 1); }
 EXPORT float or_e4m3_widen(uint8_t b) { return widen_fmt(b, 4, 3, 0, 1); }
+
+/* F16 (scalar.rs:114-117): IEEE binary16 through the same narrow/widen. */
+EXPORT uint16_t or_f16_narrow(float x) { return (uint16_t)narrow_fmt(x, 5, 10, 1, 1); }
+EXPORT float or_f16_widen(uint16_t b) { return widen_fmt(b, 5, 10, 1, 1); }
+
+/* E8M0 (scalar.rs:139-161): a power-of-two scale, rounded up so a block never clips;
+ * 0xFF is NaN. */
+EXPORT uint8_t or_e8m0_narrow(float x) {
+    if (isnan(x)) return 0xFF;
+    uint32_t b = f2u(fabsf(x));
+    int up = (int)(b >> 23) + ((b & 0x7FFFFF) != 0);
+    return (uint8_t)(up < 0 ? 0 : (up > 254 ? 254 : up));
+}
+EXPORT float or_e8m0_widen(uint8_t e) { return e == 0xFF ? NAN : (float)pow2d((int)e - 127); }
+
+/* ------------------------------------------------------------------ */
+/* Block forms: engine/ir/mem/src/block.rs:1-291                       */
+/* ------------------------------------------------------------------ */
+/* form 0 = q8_0 (F16 scale, I8 codes, halves), 1 = mxfp8 (E8M0 scale, E4M3 codes),
+ * 2 = int4_g32 (F16 scale, Nibble codes, adjacent pairs); 32 codes a block, no head. */
+static int blk_scale_bytes(int form) { return form == 1 ? 1 : 2; }
+static int blk_bits(int form) { return form == 2 ? 4 : 8; }
+EXPORT int or_block_bytes(int form) { return blk_scale_bytes(form) + 32 * blk_bits(form) / 8; }
+
+/* place (block.rs:131-137): 8-bit codes at byte j; nibbles paired by halves (j % 16,
+ * shift 4 (j / 16)) or adjacent (j / 2, shift 4 (j % 2)). */
+static void blk_place(int form, int j, int *byte, int *shift) {
+    if (blk_bits(form) == 8) { *byte = j; *shift = 0; return; }
+    *byte = j / 2; *shift = 4 * (j % 2); /* int4_g32: halves = false */
+}
+static float blk_decode(int form, uint32_t code) {
+    switch (form) {
+    case 0: return (float)(int8_t)(uint8_t)code;          /* I8 (block.rs:79-90) */
+    case 1: return or_e4m3_widen((uint8_t)code);           /* E4M3 (block.rs:66-76) */
+    default: return (float)code - 8.0f;                    /* Nibble (block.rs:95-104) */
+    }
+}
+static uint32_t blk_encode(int form, float scaled) {
+    switch (form) {
+    case 0: { /* round_ties_even, clamp to [-128, 127], as a byte */
+        float r = nearbyintf(scaled);
+        r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
+        if (isnan(scaled)) r = 0.0f; /* Rust's saturating cast: NaN -> 0 */
+        return (uint32_t)(uint8_t)(int8_t)r;
+    }
+    case 1: return or_e4m3_narrow(scaled);
+    default: { /* (scaled + 8.5).clamp(0, 15) as u32: truncation */
+        float t = scaled + 8.5f;
+        t = t < 0.0f ? 0.0f : (t > 15.0f ? 15.0f : t);
+        if (isnan(t)) t = 0.0f;
+        return (uint32_t)t;
+    }
+    }
+}
+/* Code::scale (block.rs:15-17) and Nibble::scale (block.rs:107-113). */
+static float blk_code_scale(int form, const float *b, int n) {
+    if (form == 2) {
+        float top = 0.0f;
+        for (int i = 0; i < n; i++) if (fabsf(b[i]) > fabsf(top)) top = b[i];
+        return top / -8.0f;
+    }
+    float m = 0.0f;
+    for (int i = 0; i < n; i++) m = fmaxf(m, fabsf(b[i]));
+    return m / (form == 0 ? 127.0f : 448.0f);
+}
+static void blk_put(int form, float scale, uint8_t *at) {
+    if (form == 1) { at[0] = or_e8m0_narrow(scale); return; }
+    uint16_t h = or_f16_narrow(scale);
+    at[0] = (uint8_t)h; at[1] = (uint8_t)(h >> 8);
+}
+static float blk_get(int form, const uint8_t *at) {
+    if (form == 1) return or_e8m0_widen(at[0]);
+    return or_f16_widen((uint16_t)(at[0] | (at[1] << 8)));
+}
+
+/* pack (block.rs:229-248): per block, the scale from its values, stored; codes are
+ * the values over the scale as stored (0 when it is 0). `out` must be zeroed. */
+EXPORT void or_block_pack(int form, const float *data, int64_t n, uint8_t *out) {
+    const int bb = or_block_bytes(form), sb = blk_scale_bytes(form);
+    for (int64_t b = 0; b * 32 < n; b++) {
+        const int cnt = (int)(n - b * 32 < 32 ? n - b * 32 : 32);
+        uint8_t *at = out + b * bb;
+        blk_put(form, blk_code_scale(form, data + b * 32, cnt), at);
+        const float stored = blk_get(form, at);
+        for (int j = 0; j < cnt; j++) {
+            const float scaled = stored == 0.0f ? 0.0f : data[b * 32 + j] / stored;
+            int byte, shift;
+            blk_place(form, j, &byte, &shift);
+            at[sb + byte] |= (uint8_t)(blk_encode(form, scaled) << shift);
+        }
+    }
+}
+
+/* unpack (block.rs:221-227). */
+EXPORT float or_block_unpack(int form, const uint8_t *bytes, int64_t index) {
+    const uint8_t *at = bytes + (index / 32) * or_block_bytes(form);
+    int byte, shift;
+    blk_place(form, (int)(index % 32), &byte, &shift);
+    const uint32_t code = ((uint32_t)at[blk_scale_bytes(form) + byte] >> shift) & ((1u << blk_bits(form)) - 1);
+    return blk_get(form, at) * blk_decode(form, code);
+}
+
+/* dot (block.rs:202-219): per block, part = sum_j x_j decode(c_j) from 0.0 in j order;
+ * sum += scale * part in block order; times the head (1.0 for these forms). */
+EXPORT float or_block_dot(int form, const float *x, const uint8_t *bytes, int64_t n) {
+    const int bb = or_block_bytes(form), sb = blk_scale_bytes(form);
+    const uint32_t mask = (1u << blk_bits(form)) - 1;
+    float sum = 0.0f;
+    for (int64_t b = 0; b * 32 < n; b++) {
+        const uint8_t *at = bytes + b * bb;
+        float part = 0.0f;
+        for (int j = 0; j < 32 && b * 32 + j < n; j++) {
+            int byte, shift;
+            blk_place(form, j, &byte, &shift);
+            const float prod = x[b * 32 + j] * blk_decode(form, ((uint32_t)at[sb + byte] >> shift) & mask);
+            part = part + prod;
+        }
+        const float sp = blk_get(form, at) * part;
+        sum = sum + sp;
+    }
+    return 1.0f * sum;
+}
+
+/* out[m, r] = dot(x[m], row r) for rows packed one after another (k a multiple of 32). */
+EXPORT void or_block_product(int form, int64_t m, int64_t n, int64_t k, const float *x, const uint8_t *w,
+                             float *out) {
+    const int64_t rb = k / 32 * or_block_bytes(form);
+#pragma omp parallel for num_threads(g_threads) schedule(static)
+    for (int64_t r = 0; r < n; r++)
+        for (int64_t i = 0; i < m; i++) out[i * n + r] = or_block_dot(form, x + i * k, w + r * rb, k);
+}
 
 EXPORT void or_bf16_narrow_n(const float *x, uint16_t *out, int64_t n) {
     for (int64_t i = 0; i < n; i++) out[i] = or_bf16_narrow(x[i]);

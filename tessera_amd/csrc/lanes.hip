@@ -396,7 +396,7 @@ int check(const ts_linear_args *a) {
 }  // namespace
 
 extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
-    if (!a || a->m <= 4 || a->m > 64) return 0;
+    if (!a || a->m <= 4 || a->m > 64 || ts::block_form(a->w_dtype)) return 0;
     const Plan pl = plan(a);
     if (pl.splits <= 1) return 0;
     const size_t per = (size_t)a->m * a->n * ((a->stages & TS_AFTER_SILU_MUL) ? 2 : 1);
@@ -404,6 +404,7 @@ extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
 }
 
 extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
+    if (a && ts::block_form(a->w_dtype)) return ts::block_gemv_launch(a, stream);
     int rc = check(a);
     if (rc) return rc;
     if (a->m <= 4) return ts::gemv_launch(a, stream);

@@ -55,27 +55,32 @@ def workspace(device) -> Workspace:
     return _ws[key]
 
 
-def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6):
+BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_INT4_G32}
+
+
+def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6, w_form=None):
     m, k = x.shape
     n = out.shape[1]
     a = abi.LinearArgs()
     a.x, a.w, a.w_scale, a.gain, a.a0, a.out = (_ptr(x), _ptr(w), _ptr(w_scale), _ptr(gain), _ptr(a0),
                                                 _ptr(out))
     a.m, a.n, a.k = m, n, k
-    a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
+    a.x_dtype, a.out_dtype = _DT[x.dtype], _DT[out.dtype]
+    # Block forms: w is the packed bytes [n, k / 32 * block bytes] (uint8).
+    a.w_dtype = BLOCK_FORMS[w_form] if w_form is not None else _DT[w.dtype]
     a.stages, a.eps = stages, eps
     return a
 
 
 def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, gain=None, a0=None,
-            silu_mul=False, eps=1e-6):
+            silu_mul=False, eps=1e-6, w_form=None):
     m = x.shape[0]
     n = w.shape[0] // 2 if silu_mul else w.shape[0]
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     stages = (abi.TS_AFTER_ADD if a0 is not None else 0) | (abi.TS_AFTER_SILU_MUL if silu_mul else 0) | \
         (abi.TS_BEFORE_RMS_NORM if gain is not None else 0)
-    a = linear_args(x, w, out, w_scale=w_scale, gain=gain, a0=a0, stages=stages, eps=eps)
+    a = linear_args(x, w, out, w_scale=w_scale, gain=gain, a0=a0, stages=stages, eps=eps, w_form=w_form)
     lib = abi.load()
     need = getattr(lib, fn + "_workspace")(C.byref(a)) if hasattr(lib, fn + "_workspace") else 0
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)
@@ -111,7 +116,9 @@ def picked(x, w, ids, *, n=None, repeat=1, first=0, offset=0, silu_mul=False, w_
     a = abi.PickedArgs()
     a.x, a.w, a.w_scale, a.ids, a.out = _ptr(x), _ptr(w), _ptr(w_scale), _ptr(ids), _ptr(out)
     a.rows, a.n, a.k, a.count, a.stride, a.offset, a.repeat, a.first = rows, n, k, count, stride, offset, repeat, first
-    a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
+    a.x_dtype, a.out_dtype = _DT[x.dtype], _DT[out.dtype]
+    # Block forms: w is the packed bytes [n, k / 32 * block bytes] (uint8).
+    a.w_dtype = BLOCK_FORMS[w_form] if w_form is not None else _DT[w.dtype]
     a.stages = abi.TS_AFTER_SILU_MUL if silu_mul else 0
     need = abi.load().tessera_hip_picked_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)

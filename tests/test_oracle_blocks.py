@@ -1,0 +1,103 @@
+"""The oracle's block forms (engine/ir/mem/src/block.rs) and the narrow scales they
+store (engine/ir/graph/src/scalar.rs: F16, E8M0), pinned by the reference's
+blocks_round_trip (block_test.rs:5-53), closed forms and numpy's float16."""
+import numpy as np
+import pytest
+
+import oracle as O
+
+L = O.lib()
+
+
+def test_f16_codes_round_trip_and_match_numpy():
+    codes = np.arange(1 << 16, dtype=np.uint16)
+    vals = np.array([L.or_f16_widen(int(c)) for c in codes], np.float32)
+    want = codes.view(np.float16).astype(np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(vals[finite], want[finite])          # widening = IEEE binary16
+    assert np.all(np.isnan(vals[np.isnan(want)]))
+    back = np.array([L.or_f16_narrow(float(v)) for v in vals[finite]], np.uint16)
+    assert np.array_equal(back, codes[finite])                 # every finite code round-trips
+    r = np.random.default_rng(0)
+    x = np.concatenate([r.standard_normal(20000) * s for s in (1e-7, 1e-4, 1.0, 1e3, 1e5)]).astype(np.float32)
+    got = np.array([L.or_f16_narrow(float(v)) for v in x], np.uint16)
+    assert np.array_equal(got, x.astype(np.float16).view(np.uint16))  # RNE, subnormals, overflow to inf
+
+
+@pytest.mark.parametrize("x,code", [(1.0, 127), (1.5, 128), (0.75, 127), (2.0, 128), (0.0, 0),
+                                    (2.0 ** -130, 1), (3.0e38, 254), (-4.0, 129)])
+def test_e8m0_rounds_up(x, code):
+    assert L.or_e8m0_narrow(x) == code
+    assert L.or_e8m0_widen(code) == 2.0 ** (code - 127)
+    assert L.or_e8m0_widen(code) >= abs(x) or code == 254
+
+
+def test_e8m0_nan():
+    assert L.or_e8m0_narrow(float("nan")) == 0xFF and np.isnan(L.or_e8m0_widen(0xFF))
+
+
+@pytest.mark.parametrize("form,share", [("q8_0", 0.005), ("mxfp8", 0.07), ("int4_g32", 0.07)])
+def test_blocks_round_trip(form, share):
+    """block_test.rs:5-53: round trip within a share of the largest value, byte counts,
+    and a dot equal to the plain sum over the unpacked elements."""
+    data = np.array([((i * 37) % 23) * 0.01 - 0.1 for i in range(128)], np.float32)
+    b = O.block_pack(form, data[None])[0]
+    back = O.block_unpack(form, b, 128)
+    assert np.abs(back - data).max() <= np.abs(data).max() * share
+    x = np.array([(i % 7) - 3.0 for i in range(128)], np.float32)
+    want = sum(float(x[i]) * float(back[i]) for i in range(128))
+    assert abs(O.block_dot(form, x, b) - want) <= 1e-4
+    assert b.size == {"q8_0": 136, "mxfp8": 132, "int4_g32": 72}[form]
+    assert 2 * O.block_bytes(form) == {"q8_0": 68, "mxfp8": 66, "int4_g32": 36}[form]  # bytes(64)
+
+
+def test_q8_0_closed_forms():
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    assert O.block_dot("q8_0", np.ones(32, np.float32), blk) == -16.0
+    assert O.block_dot("q8_0", np.arange(32, dtype=np.float32), blk) == 2480.0  # sum j (j - 16)
+    # pack: scale = max|x| / 127 stored as f16; codes round half to even
+    data = np.zeros(32, np.float32)
+    data[:5] = [127.0, 0.5, 1.5, 2.5, -3.5]
+    p = O.block_pack("q8_0", data[None])[0]
+    assert p[:2].view(np.float16)[0] == 1.0
+    assert list(p[2:7].view(np.int8)) == [127, 0, 2, 2, -4]
+
+
+def test_int4_g32_placement_and_sign_keeping_scale():
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[2] = 0x21  # element 0 = low nibble 1, element 1 = high nibble 2 (adjacent pairs)
+    u = O.block_unpack("int4_g32", blk, 32)
+    assert u[0] == (1 - 8) * 0.5 and u[1] == (2 - 8) * 0.5 and u[2] == -8 * 0.5
+    data = np.zeros(32, np.float32)
+    data[:3] = [4.0, -2.0, 1.0]  # widest value 4: scale 4 / -8 = -0.5, so 4 lands on code 0 (-8)
+    p = O.block_pack("int4_g32", data[None])[0]
+    assert p[:2].view(np.float16)[0] == -0.5
+    assert p[2] & 15 == 0 and O.block_unpack("int4_g32", p, 32)[0] == 4.0
+
+
+def test_mxfp8_scale_and_codes():
+    blk = np.zeros(33, np.uint8)
+    blk[0] = 128          # 2.0
+    blk[1] = 0x38         # e4m3 1.0
+    blk[2] = 0xC0         # e4m3 -2.0
+    u = O.block_unpack("mxfp8", blk, 32)
+    assert u[0] == 2.0 and u[1] == -4.0 and u[2] == 0.0
+    data = np.zeros(32, np.float32)
+    data[0] = 448.0 * 3  # scale 3 rounds up to 4 (e8m0 129); 1344 / 4 = 336 lies midway
+    p = O.block_pack("mxfp8", data[None])[0]  # between e4m3 320 and 352: ties to even, 320
+    assert p[0] == 129 and p[1] == 0x7A and O.block_unpack("mxfp8", p, 32)[0] == 1280.0
+
+
+def test_block_product_is_dot_per_row():
+    r = np.random.default_rng(3)
+    w = (r.standard_normal((5, 256)) * 0.02).astype(np.float32)
+    x = r.standard_normal((3, 256)).astype(np.float32)
+    for form in O.BLOCK_FORMS:
+        wb = O.block_pack(form, w)
+        got = O.block_product(form, x, wb)
+        for i in range(3):
+            for j in range(5):
+                assert got[i, j] == O.block_dot(form, x[i], wb[j])
