@@ -64,8 +64,8 @@ template <int FORM, int M, bool XF32>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) {
 #pragma clang fp contract(off)
     constexpr int SB = Form<FORM>::kScaleBytes, BB = Form<FORM>::kBytes;
-    __shared__ uint32_t stage[kWaves][kChunk * BB / 4];
-    __shared__ float contrib[kWaves][M][kChunk];
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kChunk * BB / 4];
+    __shared__ __attribute__((aligned(16))) float contrib[kWaves][M][kChunk];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t row = blockIdx.x * kWaves + wave;
@@ -78,7 +78,17 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
     for (uint32_t c0 = 0; c0 < nb; c0 += kChunk) {
         const uint32_t cnt = min((uint32_t)kChunk, nb - c0), words = cnt * BB / 4;
         const uint32_t *src = wrow + (size_t)c0 * BB / 4;
-        for (uint32_t i = lane; i < words; i += 64) stage[wave][i] = __builtin_nontemporal_load(src + i);
+        // Every word of the slice in flight before any is written (at most 9 a lane).
+        constexpr int kWords = (kChunk * BB / 4 + 63) / 64;
+        uint32_t wt[kWords];
+#pragma unroll
+        for (int q = 0; q < kWords; q++) {
+            const uint32_t i = lane + 64 * q;
+            wt[q] = i < words ? __builtin_nontemporal_load(src + i) : 0u;
+        }
+#pragma unroll
+        for (int q = 0; q < kWords; q++)
+            if (lane + 64 * q < words) stage[wave][lane + 64 * q] = wt[q];
         wave_lds_sync();
         if (lane < cnt) {
             const uint8_t *blk = sb + lane * BB;
@@ -134,8 +144,20 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
             }
         }
         wave_lds_sync();
-        if (lane < Mr)
-            for (uint32_t b = 0; b < cnt; b++) run = run + contrib[wave][lane][b];
+        if (lane < Mr) {  // all 64 contributions read first, then added in block order
+            const float4 *cv = (const float4 *)contrib[wave][lane];
+            float4 t[kChunk / 4];
+#pragma unroll
+            for (int q = 0; q < kChunk / 4; q++) t[q] = cv[q];
+#pragma unroll
+            for (int q = 0; q < kChunk / 4; q++)
+                if ((uint32_t)(4 * q) < cnt) {  // cnt is a multiple of 4
+                    run = run + t[q].x;
+                    run = run + t[q].y;
+                    run = run + t[q].z;
+                    run = run + t[q].w;
+                }
+        }
         wave_lds_sync();  // the next slice overwrites stage and contrib
     }
     if (lane >= Mr) return;
