@@ -7,12 +7,12 @@
 // 8 below their value, adjacent pairs per byte), block.rs:258-286, as the lanes
 // rule reads them through a form's load (engine/plan/codegen/src/form.rs:10-93).
 //
-// gfx950 design. One wave per weight row. A row is K/32 blocks of 33, 34 or 18
-// bytes, so blocks are not 16-byte aligned: the wave streams the row's bytes with
-// coalesced 4-byte loads into its own LDS slice, 64 blocks at a time, and lane l
-// then decodes block l from LDS. Each lane forms its block's part in the
+// gfx950 design. One wave per 4 weight rows. A row is K/32 blocks of 33, 34 or 18
+// bytes, so blocks are not 16-byte aligned: the wave streams its rows' bytes with
+// coalesced 4-byte loads (all four rows in flight together) into its own LDS
+// slices, 64 blocks at a time, and lane l then decodes block l of each row. Each lane forms its block's part in the
 // reference's order (x_j times the decoded code, summed from 0.0 in j order, no
-// contraction), times the block scale; lane m then adds the 64 contributions of
+// contraction), times the block scale; lane (row, m) then adds the contributions of
 // activation row m in block order. Every rounding step is the reference's, so the
 // product is bit-identical to Block::dot for the same f32 activations.
 #include "common.h"
@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kChunk = 64;  // blocks per LDS slice: one per lane
+constexpr int kRows = 4;    // weight rows per wave, their loads overlapped
 
 struct BlockParams {
     const void *x;
@@ -64,54 +65,39 @@ template <int FORM, int M, bool XF32>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) {
 #pragma clang fp contract(off)
     constexpr int SB = Form<FORM>::kScaleBytes, BB = Form<FORM>::kBytes;
-    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kChunk * BB / 4];
-    __shared__ __attribute__((aligned(16))) float contrib[kWaves][M][kChunk];
+    constexpr int kSlice = kChunk * BB / 4;                 // words of one row's slice
+    constexpr int kWords = (kSlice + 63) / 64;              // of them per lane (at most 9)
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kRows][kSlice];
+    __shared__ __attribute__((aligned(16))) float contrib[kWaves][kRows * M][kChunk];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row = blockIdx.x * kWaves + wave;
-    if (row >= p.n) return;  // waves are independent: no group barrier below
+    const uint32_t r0 = (blockIdx.x * kWaves + wave) * kRows;  // this wave's kRows rows
+    if (r0 >= p.n) return;  // waves are independent: no group barrier below
     const uint32_t K = p.k, N = p.n, Mr = p.m, nb = K / 32;
-    const uint32_t *wrow = (const uint32_t *)(p.w + (size_t)row * nb * BB);
-    const uint8_t *sb = (const uint8_t *)stage[wave];
+    const uint32_t nrows = min((uint32_t)kRows, N - r0);
 
-    float run = 0.0f;  // lane m < Mr: the running sum of output (m, row)
+    float run = 0.0f;  // lane rr * M + m: the running sum of output (m, r0 + rr)
     for (uint32_t c0 = 0; c0 < nb; c0 += kChunk) {
         const uint32_t cnt = min((uint32_t)kChunk, nb - c0), words = cnt * BB / 4;
-        const uint32_t *src = wrow + (size_t)c0 * BB / 4;
-        // Every word of the slice in flight before any is written (at most 9 a lane).
-        constexpr int kWords = (kChunk * BB / 4 + 63) / 64;
-        uint32_t wt[kWords];
+        // Every word of the rows' slices in flight before any is written.
+        uint32_t wt[kRows][kWords];
 #pragma unroll
-        for (int q = 0; q < kWords; q++) {
-            const uint32_t i = lane + 64 * q;
-            wt[q] = i < words ? __builtin_nontemporal_load(src + i) : 0u;
+        for (int rr = 0; rr < kRows; rr++) {
+            const uint32_t *src = (const uint32_t *)(p.w + (size_t)(r0 + min((uint32_t)rr, nrows - 1)) * nb * BB) +
+                                  (size_t)c0 * BB / 4;
+#pragma unroll
+            for (int q = 0; q < kWords; q++) {
+                const uint32_t i = lane + 64 * q;
+                wt[rr][q] = i < words ? __builtin_nontemporal_load(src + i) : 0u;
+            }
         }
 #pragma unroll
-        for (int q = 0; q < kWords; q++)
-            if (lane + 64 * q < words) stage[wave][lane + 64 * q] = wt[q];
+        for (int rr = 0; rr < kRows; rr++)
+#pragma unroll
+            for (int q = 0; q < kWords; q++)
+                if (lane + 64 * q < words) stage[wave][rr][lane + 64 * q] = wt[rr][q];
         wave_lds_sync();
         if (lane < cnt) {
-            const uint8_t *blk = sb + lane * BB;
-            const float scale = FORM == 1 ? e8m0_value(blk[0]) : f16_value(blk[0], blk[1]);
-            float wv[32];
-            if (FORM == 0) {
-#pragma unroll
-                for (int j = 0; j < 32; j++) wv[j] = (float)(int8_t)blk[SB + j];
-            } else if (FORM == 1) {
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    const uint32_t c = blk[SB + 4 * q] | (blk[SB + 4 * q + 1] << 8) | (blk[SB + 4 * q + 2] << 16) |
-                                       ((uint32_t)blk[SB + 4 * q + 3] << 24);
-                    e4m3x4_to_f32(c, wv + 4 * q);
-                }
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; q++) {
-                    const uint32_t b = blk[SB + q];
-                    wv[2 * q] = (float)(b & 15u) - 8.0f;
-                    wv[2 * q + 1] = (float)(b >> 4) - 8.0f;
-                }
-            }
             const uint32_t k0 = (c0 + lane) * 32;
 #pragma unroll
             for (int m = 0; m < M; m++) {
@@ -137,14 +123,38 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
                         }
                     }
                 }
-                float part = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 32; j++) part = part + xv[j] * wv[j];
-                contrib[wave][m][lane] = scale * part;
+                for (int rr = 0; rr < kRows; rr++) {
+                    const uint8_t *blk = (const uint8_t *)stage[wave][rr] + lane * BB;
+                    const float scale = FORM == 1 ? e8m0_value(blk[0]) : f16_value(blk[0], blk[1]);
+                    float wv[32];
+                    if (FORM == 0) {
+#pragma unroll
+                        for (int j = 0; j < 32; j++) wv[j] = (float)(int8_t)blk[SB + j];
+                    } else if (FORM == 1) {
+#pragma unroll
+                        for (int q = 0; q < 8; q++) {
+                            const uint32_t c = blk[SB + 4 * q] | (blk[SB + 4 * q + 1] << 8) |
+                                               (blk[SB + 4 * q + 2] << 16) | ((uint32_t)blk[SB + 4 * q + 3] << 24);
+                            e4m3x4_to_f32(c, wv + 4 * q);
+                        }
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 16; q++) {
+                            const uint32_t b = blk[SB + q];
+                            wv[2 * q] = (float)(b & 15u) - 8.0f;
+                            wv[2 * q + 1] = (float)(b >> 4) - 8.0f;
+                        }
+                    }
+                    float part = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 32; j++) part = part + xv[j] * wv[j];
+                    contrib[wave][rr * M + m][lane] = scale * part;
+                }
             }
         }
         wave_lds_sync();
-        if (lane < Mr) {  // all 64 contributions read first, then added in block order
+        if (lane < kRows * M) {  // all 64 contributions read first, then added in block order
             const float4 *cv = (const float4 *)contrib[wave][lane];
             float4 t[kChunk / 4];
 #pragma unroll
@@ -160,9 +170,10 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
         }
         wave_lds_sync();  // the next slice overwrites stage and contrib
     }
-    if (lane >= Mr) return;
+    const uint32_t rr = lane / M, m = lane % M;
+    if (lane >= kRows * M || rr >= nrows || m >= Mr) return;
     float v = 1.0f * run;  // Block::dot's head: 1.0 for these forms
-    const size_t at = (size_t)lane * N + row;
+    const size_t at = (size_t)m * N + r0 + rr;
     if (p.stages & TS_AFTER_ADD) v += p.a0[at];
     if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
     else ((float *)p.out)[at] = v;
@@ -207,7 +218,7 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     const bool xf = a->x_dtype == TS_F32;
     Kern k = a->w_dtype == TS_Q8_0 ? pick_x<0>(a->m, xf) : a->w_dtype == TS_MXFP8 ? pick_x<1>(a->m, xf)
                                                                                   : pick_x<2>(a->m, xf);
-    hipLaunchKernelGGL(k, dim3((a->n + kWaves - 1) / kWaves), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+    hipLaunchKernelGGL(k, dim3((a->n + kWaves * kRows - 1) / (kWaves * kRows)), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("lanes (block form) launch");
     return TS_OK;
 }
