@@ -116,9 +116,7 @@ def picked(x, w, ids, *, n=None, repeat=1, first=0, offset=0, silu_mul=False, w_
     a = abi.PickedArgs()
     a.x, a.w, a.w_scale, a.ids, a.out = _ptr(x), _ptr(w), _ptr(w_scale), _ptr(ids), _ptr(out)
     a.rows, a.n, a.k, a.count, a.stride, a.offset, a.repeat, a.first = rows, n, k, count, stride, offset, repeat, first
-    a.x_dtype, a.out_dtype = _DT[x.dtype], _DT[out.dtype]
-    # Block forms: w is the packed bytes [n, k / 32 * block bytes] (uint8).
-    a.w_dtype = BLOCK_FORMS[w_form] if w_form is not None else _DT[w.dtype]
+    a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
     a.stages = abi.TS_AFTER_SILU_MUL if silu_mul else 0
     need = abi.load().tessera_hip_picked_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)
