@@ -91,3 +91,15 @@ def test_attend_step_refuses_workspace_sized_for_attend_rows():
     r.workspace_bytes = 1 * 8 * 6 * 2 * 130 * 4  # attend_rows' 6 partitions at this span
     rc = lib.tessera_hip_attend_step(C.byref(r), fake, fake, fake, fake, 3000, C.c_float(1e-6), None)
     assert rc == abi.TS_ERR_WORKSPACE
+
+
+def test_dtype_enum_matches_header():
+    """The storage-type enum of include/tessera_hip.h and the binding's constants agree
+    (the block forms' values are part of the ABI)."""
+    import os
+    import re
+    text = open(os.path.join(os.path.dirname(__file__), "..", "include", "tessera_hip.h")).read()
+    enum = re.search(r"enum \{ (TS_F32 = 0[^}]*)\};", text).group(1)
+    pairs = dict((k.strip(), int(v)) for k, v in (e.split("=") for e in enum.split(",")))
+    assert pairs == {"TS_F32": abi.TS_F32, "TS_BF16": abi.TS_BF16, "TS_E4M3": abi.TS_E4M3, "TS_U32": abi.TS_U32,
+                     "TS_Q8_0": abi.TS_Q8_0, "TS_MXFP8": abi.TS_MXFP8, "TS_INT4_G32": abi.TS_INT4_G32}
