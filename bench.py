@@ -249,11 +249,11 @@ def c4(torch):
 
 
 def blocks(torch):
-    """Block-form weights on the m = 1 decode product (q8_0, mxfp8, int4_g32: 32 codes a
+    """Block-form weights on the m = 1 decode product (q8_0, mxfp8, int4_g32, q4_0: 32 codes a
     block under one scale): the Qwen3 lm_head (151936 x 1024) and the Llama-3-8B-like
     gate (14336 x 4096) shapes, HBM-bound. Bytes = packed rows + 4K (x) + 4N (out)."""
     from tessera_amd import rules
-    sizes = {"q8_0": 34, "mxfp8": 33, "int4_g32": 18}
+    sizes = {"q8_0": 34, "mxfp8": 33, "int4_g32": 18, "q4_0": 18}
     res, bytes_all, t_all = {}, 0.0, 0.0
     for shape, (K, N) in {"lm_head": (1024, 151936), "gate": (4096, 14336)}.items():
         x = torch.randn((1, K), device="cuda")

@@ -38,9 +38,11 @@ extern "C" {
  * scale then 32 codes, rows back to back (k a multiple of 128); w_scale is unused:
  *   TS_Q8_0      34 B a block: f16 scale, 32 signed bytes
  *   TS_MXFP8     33 B a block: e8m0 scale, 32 e4m3 codes
- *   TS_INT4_G32  18 B a block: f16 scale, 32 nibbles (code - 8), low nibble first
+ *   TS_INT4_G32  18 B a block: f16 scale, 32 nibbles (code - 8), element 2q low, 2q+1 high
+ *   TS_Q4_0      18 B a block: f16 scale, 32 nibbles (code - 8), element q low, q+16 high
  * They are accepted by tessera_hip_lanes / tessera_hip_linear for m <= 4 rows. */
-enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 = 5, TS_INT4_G32 = 6 };
+enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 = 5, TS_INT4_G32 = 6,
+       TS_Q4_0 = 7 };
 
 /* Fused stages around a product (engine/plan/lower/src/kernels/map.rs:20-59 MapStage,
  * applied by `finish` at the store, map.rs:155-185). */

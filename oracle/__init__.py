@@ -337,7 +337,7 @@ def mix(x, weights=None) -> np.ndarray:
 # --- block forms: engine/ir/mem/src/block.rs:1-291 --------------------------------
 # Each form: 32 codes after one scale per block, no head. Rows of a [n, k] matrix are
 # packed one after another (k a multiple of 32, so blocks never straddle rows).
-BLOCK_FORMS = {"q8_0": 0, "mxfp8": 1, "int4_g32": 2}
+BLOCK_FORMS = {"q8_0": 0, "mxfp8": 1, "int4_g32": 2, "q4_0": 3}
 
 
 def block_bytes(form: str) -> int:

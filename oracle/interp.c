@@ -128,22 +128,24 @@ EXPORT float or_e8m0_widen(uint8_t e) { return e == 0xFF ? NAN : (float)pow2d((i
 /* Block forms: engine/ir/mem/src/block.rs:1-291                       */
 /* ------------------------------------------------------------------ */
 /* form 0 = q8_0 (F16 scale, I8 codes, halves), 1 = mxfp8 (E8M0 scale, E4M3 codes),
- * 2 = int4_g32 (F16 scale, Nibble codes, adjacent pairs); 32 codes a block, no head. */
+ * 2 = int4_g32 (F16 scale, Nibble codes, adjacent pairs), 3 = q4_0 (F16 scale, Nibble
+ * codes paired by halves); 32 codes a block, no head. */
 static int blk_scale_bytes(int form) { return form == 1 ? 1 : 2; }
-static int blk_bits(int form) { return form == 2 ? 4 : 8; }
+static int blk_bits(int form) { return form >= 2 ? 4 : 8; }
 EXPORT int or_block_bytes(int form) { return blk_scale_bytes(form) + 32 * blk_bits(form) / 8; }
 
 /* place (block.rs:131-137): 8-bit codes at byte j; nibbles paired by halves (j % 16,
  * shift 4 (j / 16)) or adjacent (j / 2, shift 4 (j % 2)). */
 static void blk_place(int form, int j, int *byte, int *shift) {
     if (blk_bits(form) == 8) { *byte = j; *shift = 0; return; }
-    *byte = j / 2; *shift = 4 * (j % 2); /* int4_g32: halves = false */
+    if (form == 3) { *byte = j % 16; *shift = 4 * (j / 16); return; } /* q4_0: halves = true */
+    *byte = j / 2; *shift = 4 * (j % 2);                              /* int4_g32: halves = false */
 }
 static float blk_decode(int form, uint32_t code) {
     switch (form) {
     case 0: return (float)(int8_t)(uint8_t)code;          /* I8 (block.rs:79-90) */
     case 1: return or_e4m3_widen((uint8_t)code);           /* E4M3 (block.rs:66-76) */
-    default: return (float)code - 8.0f;                    /* Nibble (block.rs:95-104) */
+    default: return (float)code - 8.0f;                    /* Nibble (block.rs:95-104), q4_0 and int4_g32 */
     }
 }
 static uint32_t blk_encode(int form, float scaled) {
@@ -165,7 +167,7 @@ static uint32_t blk_encode(int form, float scaled) {
 }
 /* Code::scale (block.rs:15-17) and Nibble::scale (block.rs:107-113). */
 static float blk_code_scale(int form, const float *b, int n) {
-    if (form == 2) {
+    if (form >= 2) {
         float top = 0.0f;
         for (int i = 0; i < n; i++) if (fabsf(b[i]) > fabsf(top)) top = b[i];
         return top / -8.0f;

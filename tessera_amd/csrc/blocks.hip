@@ -1,10 +1,11 @@
-// Block-scaled weight forms on the decode product (m <= 4 rows): q8_0, mxfp8 and
-// int4_g32, each 32 codes under one narrow scale.
+// Block-scaled weight forms on the decode product (m <= 4 rows): q8_0, mxfp8,
+// int4_g32 and q4_0, each 32 codes under one narrow scale.
 //
 // Replaces the decode of a block form inside the few-row product: the reference's
 // Block::dot (engine/ir/mem/src/block.rs:202-219) with the forms Q8_0 (f16 scale,
 // signed bytes), MXFP8 (e8m0 scale, e4m3 codes) and INT4_G32 (f16 scale, nibbles
-// 8 below their value, adjacent pairs per byte), block.rs:258-286, as the lanes
+// 8 below their value, adjacent pairs per byte) and Q4_0 (the same nibbles paired
+// by halves: element j in byte j % 16, high nibble for j >= 16), block.rs:258-286, as the lanes
 // rule reads them through a form's load (engine/plan/codegen/src/form.rs:10-93).
 //
 // gfx950 design. One wave per 4 weight rows. A row is K/32 blocks of 33, 34 or 18
@@ -35,11 +36,11 @@ struct BlockParams {
     int out_bf16;
 };
 
-// FORM: 0 q8_0, 1 mxfp8, 2 int4_g32.
+// FORM: 0 q8_0, 1 mxfp8, 2 int4_g32, 3 q4_0.
 template <int FORM>
 struct Form {
     static constexpr int kScaleBytes = FORM == 1 ? 1 : 2;
-    static constexpr int kBytes = kScaleBytes + (FORM == 2 ? 16 : 32);
+    static constexpr int kBytes = kScaleBytes + (FORM >= 2 ? 16 : 32);
 };
 
 // f16 scale, little-endian (exact widening, subnormals included).
@@ -138,12 +139,19 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
                                                (blk[SB + 4 * q + 2] << 16) | ((uint32_t)blk[SB + 4 * q + 3] << 24);
                             e4m3x4_to_f32(c, wv + 4 * q);
                         }
-                    } else {
+                    } else if (FORM == 2) {  // adjacent pairs: element 2q low, 2q + 1 high
 #pragma unroll
                         for (int q = 0; q < 16; q++) {
                             const uint32_t b = blk[SB + q];
                             wv[2 * q] = (float)(b & 15u) - 8.0f;
                             wv[2 * q + 1] = (float)(b >> 4) - 8.0f;
+                        }
+                    } else {  // halves: element q low, q + 16 high
+#pragma unroll
+                        for (int q = 0; q < 16; q++) {
+                            const uint32_t b = blk[SB + q];
+                            wv[q] = (float)(b & 15u) - 8.0f;
+                            wv[q + 16] = (float)(b >> 4) - 8.0f;
                         }
                     }
                     float part = 0.0f;
@@ -194,10 +202,12 @@ Kern pick_x(uint32_t m, bool xf) {
 
 }  // namespace
 
-bool block_form(int32_t dtype) { return dtype == TS_Q8_0 || dtype == TS_MXFP8 || dtype == TS_INT4_G32; }
+bool block_form(int32_t dtype) {
+    return dtype == TS_Q8_0 || dtype == TS_MXFP8 || dtype == TS_INT4_G32 || dtype == TS_Q4_0;
+}
 
 size_t block_row_bytes(int32_t dtype, uint32_t k) {
-    const size_t bb = dtype == TS_Q8_0 ? Form<0>::kBytes : dtype == TS_MXFP8 ? Form<1>::kBytes : Form<2>::kBytes;
+    const size_t bb = dtype == TS_Q8_0 ? Form<0>::kBytes : dtype == TS_MXFP8 ? Form<1>::kBytes : Form<2>::kBytes;  // q4_0: 18 as int4_g32
     return (size_t)(k / 32) * bb;
 }
 
@@ -216,8 +226,9 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     const bool xf = a->x_dtype == TS_F32;
-    Kern k = a->w_dtype == TS_Q8_0 ? pick_x<0>(a->m, xf) : a->w_dtype == TS_MXFP8 ? pick_x<1>(a->m, xf)
-                                                                                  : pick_x<2>(a->m, xf);
+    Kern k = a->w_dtype == TS_Q8_0    ? pick_x<0>(a->m, xf)
+           : a->w_dtype == TS_MXFP8   ? pick_x<1>(a->m, xf)
+           : a->w_dtype == TS_INT4_G32 ? pick_x<2>(a->m, xf) : pick_x<3>(a->m, xf);
     hipLaunchKernelGGL(k, dim3((a->n + kWaves * kRows - 1) / (kWaves * kRows)), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("lanes (block form) launch");
     return TS_OK;

@@ -55,7 +55,7 @@ def workspace(device) -> Workspace:
     return _ws[key]
 
 
-BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_INT4_G32}
+BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_INT4_G32, "q4_0": abi.TS_Q4_0}
 
 
 def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6, w_form=None):

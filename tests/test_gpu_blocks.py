@@ -22,7 +22,7 @@ def _case(form, m, n, k, seed, x_bf16=False):
     return x, x, wb
 
 
-@pytest.mark.parametrize("form", ["q8_0", "mxfp8", "int4_g32"])
+@pytest.mark.parametrize("form", ["q8_0", "mxfp8", "int4_g32", "q4_0"])
 @pytest.mark.parametrize("m,n,k", [(1, 2048, 1024), (2, 300, 3072), (3, 37, 8192), (4, 1024, 128), (1, 151936, 1024)])
 def test_block_product_bit_exact(form, m, n, k):
     from tessera_amd import rules as R
@@ -32,7 +32,7 @@ def test_block_product_bit_exact(form, m, n, k):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("form", ["q8_0", "mxfp8", "int4_g32"])
+@pytest.mark.parametrize("form", ["q8_0", "mxfp8", "int4_g32", "q4_0"])
 def test_block_product_bf16_rows_add_and_bf16_out(form):
     from tessera_amd import rules as R
     m, n, k = 2, 1000, 2048

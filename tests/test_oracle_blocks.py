@@ -36,7 +36,7 @@ def test_e8m0_nan():
     assert L.or_e8m0_narrow(float("nan")) == 0xFF and np.isnan(L.or_e8m0_widen(0xFF))
 
 
-@pytest.mark.parametrize("form,share", [("q8_0", 0.005), ("mxfp8", 0.07), ("int4_g32", 0.07)])
+@pytest.mark.parametrize("form,share", [("q8_0", 0.005), ("mxfp8", 0.07), ("int4_g32", 0.07), ("q4_0", 0.07)])
 def test_blocks_round_trip(form, share):
     """block_test.rs:5-53: round trip within a share of the largest value, byte counts,
     and a dot equal to the plain sum over the unpacked elements."""
@@ -47,8 +47,8 @@ def test_blocks_round_trip(form, share):
     x = np.array([(i % 7) - 3.0 for i in range(128)], np.float32)
     want = sum(float(x[i]) * float(back[i]) for i in range(128))
     assert abs(O.block_dot(form, x, b) - want) <= 1e-4
-    assert b.size == {"q8_0": 136, "mxfp8": 132, "int4_g32": 72}[form]
-    assert 2 * O.block_bytes(form) == {"q8_0": 68, "mxfp8": 66, "int4_g32": 36}[form]  # bytes(64)
+    assert b.size == {"q8_0": 136, "mxfp8": 132, "int4_g32": 72, "q4_0": 72}[form]
+    assert 2 * O.block_bytes(form) == {"q8_0": 68, "mxfp8": 66, "int4_g32": 36, "q4_0": 36}[form]  # bytes(64)
 
 
 def test_q8_0_closed_forms():
@@ -101,3 +101,13 @@ def test_block_product_is_dot_per_row():
         for i in range(3):
             for j in range(5):
                 assert got[i, j] == O.block_dot(form, x[i], wb[j])
+
+
+def test_q4_0_pairs_by_halves():
+    """Q4_0 (block.rs:263-266, place :131-137): element j in byte j % 16, the high nibble
+    for j >= 16; int4_g32 pairs adjacent elements instead."""
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2] = 0x21
+    u = O.block_unpack("q4_0", blk, 32)
+    assert u[0] == 1 - 8 and u[16] == 2 - 8 and u[1] == -8 and u[17] == -8
