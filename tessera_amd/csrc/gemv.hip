@@ -300,18 +300,6 @@ Kern pick_m(uint32_t m, int r) {
 // Rows per group and waves per group for a product shape: enough waves to
 // cover the chip (~2048), whole k steps per wave.
 void gemv_plan(uint32_t n, uint32_t k, bool silu, bool w8, int *rows, uint32_t *waves, uint32_t *groups) {
-    // TESSERA_GEMV_PLAN="rows,waves" pins the choice (for tuning sweeps).
-    static const char *pin = getenv("TESSERA_GEMV_PLAN");
-    if (pin) {
-        int r = 0, w = 0;
-        if (sscanf(pin, "%d,%d", &r, &w) == 2 && (r == 2 || r == 4 || r == 8) && w >= 1 && w <= 4) {
-            const uint32_t outs = silu ? r / 2 : r;
-            *rows = r;
-            *waves = (uint32_t)w;
-            *groups = (n + outs - 1) / outs;
-            return;
-        }
-    }
     // Measured on MI355X (graph-replayed, cold weights): for bf16 weights one wave
     // per group is fastest at every decode shape (an LDS exchange costs more than it
     // saves), and rows per wave grow with the row count: 8 for >= 3072 rows of 1024,
