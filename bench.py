@@ -217,7 +217,7 @@ def c3_prefill(torch):
     tab = torch.from_numpy(table).cuda()
     out = torch.empty(q.shape, device="cuda")
     fn = lambda: rules.flash_rows(q, k, v, slots, pos, keys=n, scale=width ** -0.5, table=tab,
-                                  kept_pages=kept_pages, page=page, out=out)
+                                  kept_pages=kept_pages, page=page, max_position=n - 1, out=out)
     t = _graph_time(torch, fn, launches=5)
     flops = seqs * heads * (n * (n + 1) // 2) * 4 * width
     return {"bound": "mfma", "us": round(t * 1e6, 2), "tflops": round(flops / t / 1e12, 1),

@@ -51,7 +51,7 @@ enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 =
 #define TS_BEFORE_RMS_NORM 4u /* x rows pass through RmsNorm with `gain` before the product */
 
 /* Version of this ABI; bumped on any struct layout change. */
-#define TS_ABI_VERSION 1
+#define TS_ABI_VERSION 2
 
 /* Checks that the current device is gfx950 and records its properties.
  * Replaces: the platform probe of engine/gpu/gpukit/src/rocm/context.rs:60-106
@@ -171,7 +171,15 @@ typedef struct {
     float scale;
     int32_t q_dtype, kv_dtype, out_dtype;
     uint32_t max_position;      /* an upper bound on positions[] (sizes the split) */
+    uint32_t *status;           /* device word or NULL: TS_STATUS_* bits are OR-ed in */
 } ts_rows_args;
+
+/* Device-side refusals of the attention kernels (ts_rows_args.status). A row whose
+ * position is >= keys, > max_position, or past its slot's kept_pages * page is refused,
+ * as the interpreter refuses a read at >= keys (engine/ir/interp/src/cpu.rs:323-327):
+ * the row loads nothing, writes NaN outputs (and appends nothing), and the bit below is
+ * set in *status. The caller clears the word and reads it back when it wants to know. */
+#define TS_STATUS_POSITION 1u
 
 /* Decode: few rows, each key range split across workgroups, partial
  * (max, sum, acc) merged by the last group to finish.
@@ -195,11 +203,12 @@ int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float
                             const float *k_gain, const float *rope_table, uint32_t rope_rows, float eps,
                             void *stream);
 
-/* Prefill: 64-row query blocks of one slot on the matrix unit, keys streamed
- * page by page with online softmax.
+/* Prefill: 128-row query blocks on the matrix unit, keys streamed page by page
+ * with online softmax. Rows may be packed ragged, back to back: a block whose rows
+ * belong to several slots takes one pass over the keys per distinct slot, as the
+ * reference does.
  * Replaces: rule "flash" / flash_rows (engine/rules/attention/src/flash.rs:416-503,
- * 506-591, 595-807). Rows must come in runs of one slot at consecutive positions
- * (the prefill shape); each 64-row block must not cross a slot. */
+ * 506-591, 595-807). */
 int tessera_hip_flash_rows(const ts_rows_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------

@@ -20,6 +20,8 @@ TS_ERR_ARG = -1
 TS_ERR_ARCH = -2
 TS_ERR_WORKSPACE = -3
 
+TS_STATUS_POSITION = 1  # ts_rows_args.status: a row's position was refused
+
 TS_F32, TS_BF16, TS_E4M3, TS_U32 = 0, 1, 2, 3
 TS_Q8_0, TS_MXFP8, TS_INT4_G32, TS_Q4_0 = 4, 5, 6, 7  # block forms (engine/ir/mem/src/block.rs:258-286)
 
@@ -51,7 +53,7 @@ class RowsArgs(C.Structure):
         ("rows", C.c_uint32), ("keys", C.c_uint32), ("heads", C.c_uint32), ("kv_heads", C.c_uint32),
         ("width", C.c_uint32), ("back", C.c_uint32), ("kept_pages", C.c_uint32), ("page", C.c_uint32),
         ("scale", C.c_float), ("q_dtype", C.c_int32), ("kv_dtype", C.c_int32), ("out_dtype", C.c_int32),
-        ("max_position", C.c_uint32),
+        ("max_position", C.c_uint32), ("status", C.c_void_p),
     ]
 
 

@@ -66,12 +66,35 @@ struct RowsParams {
     const float *rope;  // [positions][64] (cos, sin) pairs
     float eps;
     uint64_t *marks;    // TS_MARK ledger (debug builds)
+    uint32_t max_position;
+    uint32_t *status;   // TS_STATUS_* bits, or NULL
 };
 
 TS_DEV uint64_t kept_row(const RowsParams &p, uint32_t slot, uint32_t pos) {
     if (!p.table) return (uint64_t)slot * p.keys + pos;
     const uint64_t entry = (uint64_t)slot * p.kept_pages + (pos >> p.page_shift);
     return ((uint64_t)p.table[entry] << p.page_shift) | (pos & ((1u << p.page_shift) - 1));
+}
+
+// A row the slot cannot hold (the interpreter refuses a read at >= keys,
+// engine/ir/interp/src/cpu.rs:323-327), past the stated bound that sized the split,
+// or past the slot's table row.
+TS_DEV bool refused(const RowsParams &p, uint32_t pos) {
+    return pos >= p.keys || pos > p.max_position || (p.table && (pos >> p.page_shift) >= p.kept_pages);
+}
+
+// A refused row loads nothing: its output is NaN (directly, or as an empty partial
+// that the merge turns into 0 / 0), and the refusal is reported in *status.
+TS_DEV void refuse_row(const RowsParams &p, uint32_t r, uint32_t kvh, uint32_t part, uint32_t parts, uint32_t G) {
+    if (threadIdx.x == 0 && p.status) atomicOr(p.status, TS_STATUS_POSITION);
+    const size_t gi = (size_t)r * p.kv_heads + kvh;
+    for (uint32_t e = threadIdx.x; e < G * 130; e += blockDim.x) {
+        if (parts == 1) {
+            if (e < G * 128) p.out[((size_t)r * p.heads + kvh * G + e / 128) * 128 + e % 128] = __builtin_nanf("");
+        } else {
+            p.partials[(gi * parts + part) * G * 130 + e] = (e % 130 == 0) ? -INFINITY : 0.0f;
+        }
+    }
 }
 
 // RmsNorm over one 128-wide head held as (d, d+64) in lane d of a wave, then
@@ -103,6 +126,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
 
     TS_MARK(p.marks, 0);
     const uint32_t pos = p.positions[r], slot = p.slots[r];
+    if (refused(p, pos)) {  // uniform: one row per group
+        refuse_row(p, r, kvh, part, parts, G);
+        return;
+    }
     const uint32_t from = pos > p.back ? pos - p.back : 0;
     const uint32_t wk0 = (part * waves + wave) * (16 * NB);
     const uint32_t pmask = (1u << p.page_shift) - 1;
@@ -377,6 +404,10 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
     __shared__ uint32_t stab[kLongPages];
 
     const uint32_t pos = p.positions[r], slot = p.slots[r];
+    if (refused(p, pos)) {  // uniform: one row per group
+        refuse_row(p, r, kvh, part, parts, G);
+        return;
+    }
     const uint32_t from = pos > p.back ? pos - p.back : 0;
     const uint32_t span_keys = kLongWaves * 32 * iters;  // keys of one group
     const uint32_t g0 = part * span_keys, g1 = g0 + span_keys;
@@ -642,7 +673,7 @@ int check(const ts_rows_args *a) {
                "attend_rows: q f32, kept rows bf16, out f32 supported");
     TS_REQUIRE(!a->kept_table || (a->page >= 16 && (a->page & (a->page - 1)) == 0),
                "attend_rows: page %u must be a power of two >= 16", a->page);
-    TS_REQUIRE(a->kept_table || a->keys >= 1, "attend_rows: dense kept rows need keys");
+    TS_REQUIRE(a->keys >= 1, "attend_rows: keys (the positions a slot holds) must be >= 1");
     TS_REQUIRE(ts::aligned(a->k, 16) && ts::aligned(a->v, 16) && ts::aligned(a->q, 16),
                "attend_rows: q, k, v must be 16-byte aligned");
     TS_REQUIRE(a->kv_heads <= 65535 && a->rows <= 65535, "attend_rows: grid limits");
@@ -683,6 +714,7 @@ int launch_rows(const ts_rows_args *a, RowsParams &p, void *stream) {
     p.G = a->heads / a->kv_heads; p.back = a->back; p.kept_pages = a->kept_pages;
     p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
     p.wave_keys = s.wave_keys; p.scale = a->scale;
+    p.max_position = a->max_position; p.status = a->status;
     p.partials = nullptr;
 #ifdef TS_MARKS
     p.marks = ts_debug_marks();

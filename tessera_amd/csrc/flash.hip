@@ -13,9 +13,11 @@
 //    covers both heads of the pair. Each K/V block is loaded and staged once for all
 //    of that MFMA work: the staging is VALU work, and VALU, not the matrix unit,
 //    bounds this kernel (64 rows and one head per group measured 1.8x slower).
-//  * Rows come in 64-row blocks of one slot (the prefill shape: runs of one slot).
-//    When the group's two 64-row halves belong to different slots, the group takes
-//    one pass over each half's keys, the other half's waves idle through it.
+//  * Rows may be packed ragged (prompts back to back): a group whose rows belong to
+//    several slots makes one pass over the keys per distinct slot, in order of first
+//    appearance, as the reference's flash_rows does (flash.rs:504-591); a pass
+//    touches only its own rows' softmax state, and waves with none of them idle
+//    through it. The common case, one slot per group, is one pass.
 //  * Keys stream in 64-row blocks. K and V go to LDS as rows ([key][d], 16-byte
 //    chunks XOR-swizzled by key), 16 bytes per lane, no reshuffling: the V^T operand
 //    of O^T += V^T P^T comes out of LDS already transposed through gfx950's
@@ -41,8 +43,9 @@ struct FlashParams {
     const uint16_t *k, *v;
     float *out;
     const uint32_t *slots, *positions, *table;
-    uint32_t rows, keys, heads, kv_heads, back, kept_pages, page_shift;
+    uint32_t rows, keys, heads, kv_heads, back, kept_pages, page_shift, max_position;
     float scale;
+    uint32_t *status;
 };
 
 TS_DEV uint64_t kept_row(const FlashParams &p, uint32_t slot, uint32_t pos) {
@@ -126,8 +129,10 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     constexpr int kC = kKeys * 16 / (256 * HG);  // 16-byte K (and V) loads per thread and block
     __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
     __shared__ __attribute__((aligned(16))) uint16_t sv[kKeys][128];     // V rows, swizzled as K
-    __shared__ uint32_t srange[kQT][2];     // key range of each 64-row half
-    __shared__ uint32_t smixed;             // the halves belong to different slots
+    __shared__ uint32_t srange[kRows][2];   // key range of each pass
+    __shared__ uint32_t sslot[kRows];       // slot of each row; then the slot of each pass
+    __shared__ uint32_t spass[kRows];       // pass of each row (kNoPass: dead or refused)
+    __shared__ uint32_t snpass, smixed;
     __shared__ uint32_t stab_s[kMaxPages];  // this group's page-table entries
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
@@ -135,34 +140,85 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     const uint32_t G = p.heads / p.kv_heads, h = blockIdx.y * HG + (wave >> 2), kvh = h / G;
     const uint32_t qw = wave & 3;  // the wave's 16 kQT rows within the group's kRows
     const uint32_t r0 = blockIdx.x * kRows;
-    const uint32_t half = qw * kQT / 4;  // the 64-row half of the group holding the wave's rows
+    constexpr uint32_t kNoPass = 0xffffffffu;
 
-    // Key range of each 64-row half, and whether the halves share a slot.
-    if (t < kQT) { srange[t][0] = 0xffffffffu; srange[t][1] = 0; }
-    if (t == 0) smixed = 0;
+    // Passes: one per distinct slot among the group's rows, numbered in order of first
+    // appearance. A row the slot cannot hold (position >= keys, past the stated bound
+    // or past the slot's table row: the interpreter refuses such reads,
+    // engine/ir/interp/src/cpu.rs:323-327) takes no pass, loads nothing, writes NaN and
+    // sets the status bit.
+    bool ok_t = false;
+    uint32_t slot_t = 0;
+    if (t < kRows) {
+        srange[t][0] = 0xffffffffu;
+        srange[t][1] = 0;
+        spass[t] = kNoPass;
+        if (r0 + t < p.rows) {
+            const uint32_t pos = p.positions[r0 + t];
+            ok_t = !(pos >= p.keys || pos > p.max_position || (p.table && (pos >> p.page_shift) >= p.kept_pages));
+            if (!ok_t && p.status) atomicOr(p.status, TS_STATUS_POSITION);
+            slot_t = p.slots[r0 + t];
+        }
+    }
+    if (t == 0) { smixed = 0; snpass = 0; }
     __syncthreads();
-    if (t < kRows && r0 + t < p.rows) {
-        const uint32_t pos = p.positions[r0 + t];
-        atomicMin(&srange[t / 64][0], pos > p.back ? pos - p.back : 0);
-        atomicMax(&srange[t / 64][1], pos);
-        if (p.slots[r0 + t] != p.slots[r0]) smixed = 1;
+    if (t < kRows) sslot[t] = ok_t ? slot_t : 0;
+    if (t < kRows && ok_t) spass[t] = 0;  // provisional: whether the row is served
+    __syncthreads();
+    const uint32_t lead0 = [&] {  // first served row's slot (any, when none is served)
+        for (uint32_t j = 0; j < kRows; j++)
+            if (spass[j] == 0) return sslot[j];
+        return 0u;
+    }();
+    if (ok_t && slot_t != lead0) smixed = 1;
+    __syncthreads();
+    if (!smixed) {
+        if (t == 0) snpass = 1;
+        if (t < kRows && ok_t) spass[t] = 0;
+    } else {
+        // The leader of a row: the first served row of its slot. Leaders count the
+        // leaders before them (their pass); each row then takes its leader's pass.
+        uint32_t leader = kNoPass;
+        if (t < kRows && ok_t) {
+            for (uint32_t j = 0; j <= t; j++)
+                if (spass[j] != kNoPass && sslot[j] == slot_t) { leader = j; break; }
+        }
+        __syncthreads();
+        // Reuse spass: 1 marks a leader.
+        if (t < kRows) spass[t] = (ok_t && leader == t) ? 1u : 0u;
+        __syncthreads();
+        uint32_t mine = kNoPass;
+        if (t < kRows && ok_t) {
+            mine = 0;
+            for (uint32_t j = 0; j < leader; j++) mine += spass[j];
+        }
+        __syncthreads();
+        if (t < kRows) spass[t] = mine;
+        if (t < kRows && ok_t && leader == t) atomicAdd(&snpass, 1u);
+        __syncthreads();
+        if (t < kRows && ok_t && leader == t) sslot[mine] = slot_t;  // pass -> slot (mine <= t)
     }
     __syncthreads();
-    // Rows come in 64-row blocks of one slot. Halves of one slot share every key
-    // block (one pass); halves of two slots take a pass each, the other half's waves
-    // idle through it with no live rows.
-    const uint32_t npass = smixed ? kQT : 1;
+    if (!smixed && t == 0) sslot[0] = lead0;
+    if (t < kRows && ok_t) {
+        const uint32_t pos = p.positions[r0 + t];
+        atomicMin(&srange[spass[t]][0], pos > p.back ? pos - p.back : 0);
+        atomicMax(&srange[spass[t]][1], pos);
+    }
+    __syncthreads();
+    const uint32_t npass = snpass;
 
     // This wave's queries: r0 + 16 kQT wave + 16 qt + col. The q operand
     // (B, columns = queries), loaded once: lane group g holds d 32 g + 8 j .. + 8 for
     // d-step j; bf16 q as is, f32 q as two exact bf16 parts.
     u32x4 qh[kQT][4], ql[kQT][4];
-    uint32_t rpos[kQT], rfrom[kQT];
-    bool rlive[kQT];
+    uint32_t rpos[kQT], rfrom[kQT], rpass[kQT];
+    bool rlive[kQT];  // the row is served (exists and is not refused)
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) {
-        const uint32_t r = r0 + 16 * kQT * qw + 16 * qt + col;
-        rlive[qt] = r < p.rows;
+        const uint32_t i = 16 * kQT * qw + 16 * qt + col, r = r0 + i;
+        rpass[qt] = spass[i];
+        rlive[qt] = rpass[qt] != kNoPass;
         rpos[qt] = rlive[qt] ? p.positions[r] : 0;
         rfrom[qt] = rpos[qt] > p.back ? rpos[qt] - p.back : 0;
         if (!QF32) {
@@ -201,17 +257,12 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         for (int d = 0; d < 8; d++) o[qt][d] = f32x4{0, 0, 0, 0};
 
     for (uint32_t pass = 0; pass < npass; pass++) {
-    if (r0 + 64 * pass >= p.rows) break;
-    const uint32_t slot = p.slots[r0 + 64 * pass];
+    const uint32_t slot = sslot[pass];
     uint32_t lo = srange[pass][0], hi = srange[pass][1];
-    if (npass == 1) {
-#pragma unroll
-        for (int i = 1; i < kQT; i++) { lo = min(lo, srange[i][0]); hi = max(hi, srange[i][1]); }
-    }
     lo &= ~(kKeys - 1);
     bool act[kQT];  // rows of this pass
 #pragma unroll
-    for (int qt = 0; qt < kQT; qt++) act[qt] = rlive[qt] && (npass == 1 || half == pass);
+    for (int qt = 0; qt < kQT; qt++) act[qt] = rlive[qt] && rpass[qt] == pass;
     bool any = false;
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) any |= act[qt];
@@ -268,7 +319,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         // A block wholly inside every query's window of the wave skips the masks.
         bool inside = true;
 #pragma unroll
-        for (int qt = 0; qt < kQT; qt++) inside &= !act[qt] || (kb + kKeys - 1 <= rpos[qt] && kb >= rfrom[qt]);
+        for (int qt = 0; qt < kQT; qt++)  // rows of other passes keep their masks
+            inside &= act[qt] ? (kb + kKeys - 1 <= rpos[qt] && kb >= rfrom[qt]) : !rlive[qt];
         inside = __builtin_amdgcn_ballot_w64(!inside) == 0;  // uniform
         bf16x8 ph[2][kQT], pl[2][kQT];
 #pragma unroll
@@ -348,13 +400,14 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 
     }  // pass
 
-    // O / l: lane (query col of tile qt) holds d = 16 dt + 4 grp + i.
+    // O / l: lane (query col of tile qt) holds d = 16 dt + 4 grp + i. Refused rows
+    // write NaN.
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) {
-        if (!rlive[qt]) continue;
         const uint32_t r = r0 + 16 * kQT * qw + 16 * qt + col;
+        if (r >= p.rows) continue;
         float *dst = p.out + ((size_t)r * p.heads + h) * 128;
-        const float inv = 1.0f / l[qt];
+        const float inv = rlive[qt] ? 1.0f / l[qt] : __builtin_nanf("");
 #pragma unroll
         for (int d = 0; d < 8; d++) *(f32x4 *)(dst + d * 16 + 4 * grp) = o[qt][d] * inv;
     }
@@ -371,7 +424,7 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
                "flash_rows: q f32 or bf16, kept rows bf16, out f32 supported");
     TS_REQUIRE(!a->kept_table || (a->page >= 16 && (a->page & (a->page - 1)) == 0),
                "flash_rows: page %u must be a power of two >= 16", a->page);
-    TS_REQUIRE(a->kept_table || a->keys >= 1, "flash_rows: dense kept rows need keys");
+    TS_REQUIRE(a->keys >= 1, "flash_rows: keys (the positions a slot holds) must be >= 1");
     TS_REQUIRE(ts::aligned(a->k, 16) && ts::aligned(a->v, 16) && ts::aligned(a->q, 16),
                "flash_rows: q, k, v must be 16-byte aligned");
     TS_REQUIRE(a->heads <= 65535, "flash_rows: grid limits");
@@ -381,7 +434,7 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
     p.out = (float *)a->out; p.slots = a->slots; p.positions = a->positions; p.table = a->kept_table;
     p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads; p.back = a->back;
     p.kept_pages = a->kept_pages; p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
-    p.scale = a->scale;
+    p.scale = a->scale; p.max_position = a->max_position; p.status = a->status;
     // Two q heads per group when the kv heads are shared in pairs (or more, evenly).
     const int hg = (a->heads / a->kv_heads) % 2 == 0 ? 2 : 1;
     const bool f32 = a->q_dtype == TS_F32;

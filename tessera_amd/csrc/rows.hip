@@ -112,6 +112,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope_append_kernel(QkParams p) {
     }
     const bool is_k = h < p.heads + p.kv_heads;
     const uint32_t kvh = is_k ? h - p.heads : h - p.heads - p.kv_heads;
+    // A position the slot cannot hold appends nothing (the interpreter refuses the
+    // write, engine/ir/interp/src/run.rs:122-198); the attention that reads it refuses
+    // the row too and reports it.
+    if (pos >= p.keys || (p.table && (pos >> p.page_shift) >= p.kept_pages)) return;
     const uint64_t row = kept_row(p.table, p.kept_pages, p.page_shift, p.keys, p.slots[r], pos);
     uint16_t *dst = (is_k ? p.k_cache : p.v_cache) + (row * p.kv_heads + kvh) * 128;
     dst[lane] = bf16_bits(a);

@@ -175,7 +175,7 @@ def moe_layer(h, router, w_in, w_out, *, top=8, shared_in=None, shared_out=None,
 
 
 def rows_args(q, k, v, out, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
-              back=abi.U32_MAX, max_position=None):
+              back=abi.U32_MAX, max_position=None, status=None):
     rows, heads, width = q.shape
     a = abi.RowsArgs()
     a.q, a.k, a.v, a.out = _ptr(q), _ptr(k), _ptr(v), _ptr(out)
@@ -186,16 +186,17 @@ def rows_args(q, k, v, out, slots, positions, *, keys, scale, table=None, kept_p
     if max_position is None:
         max_position = int(positions.max().item()) if rows else 0
     a.max_position = max_position
+    a.status = _ptr(status)  # int32 device word: TS_STATUS_* bits of refused rows
     return a
 
 
 def attend_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
-                back=abi.U32_MAX, max_position=None, out=None):
+                back=abi.U32_MAX, max_position=None, out=None, status=None):
     """Decode rows over kept K/V (rule "attend"/attend_rows; split-KV)."""
     if out is None:
         out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     a = rows_args(q, k, v, out, slots, positions, keys=keys, scale=scale, table=table,
-                  kept_pages=kept_pages, page=page, back=back, max_position=max_position)
+                  kept_pages=kept_pages, page=page, back=back, max_position=max_position, status=status)
     need = abi.load().tessera_hip_attend_rows_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(q.device).get(need)
     abi.call("tessera_hip_attend_rows", C.byref(a), _stream())
@@ -228,12 +229,14 @@ def attend_step(qkv, q_gain, k_gain, k, v, slots, positions, *, heads, keys, sca
 
 
 def flash_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages=0, page=16,
-               back=abi.U32_MAX, out=None):
-    """Prefill rows over kept K/V (rule "flash"/flash_rows)."""
+               back=abi.U32_MAX, max_position=None, out=None, status=None):
+    """Prefill rows over kept K/V (rule "flash"/flash_rows); rows may be packed ragged.
+    max_position (an upper bound on positions) defaults to their maximum (a host read:
+    pass it when capturing a graph)."""
     if out is None:
         out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
     a = rows_args(q, k, v, out, slots, positions, keys=keys, scale=scale, table=table,
-                  kept_pages=kept_pages, page=page, back=back, max_position=0)
+                  kept_pages=kept_pages, page=page, back=back, max_position=max_position, status=status)
     abi.call("tessera_hip_flash_rows", C.byref(a), _stream())
     return out
 

@@ -168,3 +168,104 @@ def test_attend_step_fused(ctx):
     # (device powf/sincosf against the host's for the rotation angle).
     assert np.array_equal(from_dev(vd)[row], vf[row])
     np.testing.assert_allclose(from_dev(kd)[row], kf[row], rtol=2 ** -7, atol=1e-6)
+
+
+def _packed(lens):
+    """Prompts packed back to back with no padding (the lowered Launch layout): rows
+    of slot s at positions 0..len-1, then the next slot's rows at once."""
+    slots, positions = [], []
+    for s_, n in enumerate(lens):
+        slots += [s_] * n
+        positions += list(range(n))
+    return slots, positions
+
+
+@pytest.mark.parametrize("lens", [[70, 130, 5], [3] * 45, [1, 2, 200, 1, 64, 63], [127, 129]])
+def test_prefill_flash_rows_packed(lens):
+    """Ragged prompts back to back: 128-row groups hold rows of several slots (up to 43
+    in one group for [3] * 45); each group makes one pass per distinct slot."""
+    c = paged_case(sum(lens) + 7, lens, pos=_packed(lens))
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("flash", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
+def test_prefill_flash_rows_interleaved_slots():
+    """Rows of two slots interleaved row by row (slots not in runs), a window of 50."""
+    n = 150
+    slots = [i % 2 for i in range(2 * n)]
+    positions = [i // 2 for i in range(2 * n)]
+    c = paged_case(31, [n, n], pos=(slots, positions))
+    np.testing.assert_allclose(run("flash", c, 0.2, back=50), want(c, 0.2, "back", 50), atol=ATOL, rtol=0)
+
+
+def test_prefill_flash_rows_packed_bf16_q():
+    """The packed layout on the bf16-q form (atol 4e-3: P rounded once to bf16)."""
+    from tessera_amd import rules as R
+    lens = [70, 130, 5]
+    c = paged_case(99, lens, pos=_packed(lens))
+    qb = O.bf16_narrow(c["q"])
+    c["q"] = O.bf16_widen(qb)
+    s = 1 / math.sqrt(128)
+    got = from_dev(R.flash_rows(to_dev(qb, torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                                to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                                keys=c["keys"], scale=s, table=to_dev(c["table"], torch, torch.int32),
+                                kept_pages=c["kept_pages"], page=c["page"]))
+    np.testing.assert_allclose(got, want(c, s), atol=4e-3, rtol=0)
+
+
+@pytest.mark.parametrize("kernel,ctxs", [("attend", [300, 40]), ("attend", [3000, 600]), ("flash", [200, 90])])
+def test_refused_positions(kernel, ctxs):
+    """A row whose position the slot cannot hold (>= keys) or beyond the stated
+    max_position is refused on the device, as the interpreter refuses a read at >= keys
+    (engine/ir/interp/src/cpu.rs:323-327): it loads nothing, its outputs are NaN and the
+    status word gets TS_STATUS_POSITION; the other rows are unchanged. [3000, 600] runs
+    the split path (partials merged by a second kernel); every kernel exits normally."""
+    from tessera_amd import abi
+    from tessera_amd import rules as R
+    if kernel == "attend":
+        pos = ([0, 1, 0, 1], [ctxs[0] - 1, ctxs[1] - 1, 0, 0])
+    else:
+        pos = ([0] * ctxs[0] + [1] * ctxs[1], list(range(ctxs[0])) + list(range(ctxs[1])))
+    c = paged_case(55 + ctxs[0], ctxs, pos=pos)
+    s = 1 / math.sqrt(128)
+    good = want(c, s)
+    bad_rows = [2, 3] if kernel == "attend" else [5, ctxs[0] + 3]
+    positions = c["positions"].copy()
+    positions[bad_rows[0]] = c["keys"]            # the slot cannot hold it
+    positions[bad_rows[1]] = c["keys"] + 1000     # past the slot's table row too
+    mp = int(c["positions"].max())
+    fn = R.attend_rows if kernel == "attend" else R.flash_rows
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = from_dev(fn(to_dev(c["q"], torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                      to_dev(c["slots"], torch, torch.int32), to_dev(positions, torch, torch.int32),
+                      keys=c["keys"], scale=s, table=to_dev(c["table"], torch, torch.int32),
+                      kept_pages=c["kept_pages"], page=c["page"], max_position=mp, status=status))
+    torch.cuda.synchronize()
+    assert int(status.item()) == abi.TS_STATUS_POSITION
+    keep = np.setdiff1d(np.arange(len(positions)), bad_rows)
+    np.testing.assert_allclose(got[keep], good[keep], atol=ATOL, rtol=0)
+    assert np.all(np.isnan(got[bad_rows]))
+    # In range, the word stays clear.
+    status.zero_()
+    fn(to_dev(c["q"], torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+       to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+       keys=c["keys"], scale=s, table=to_dev(c["table"], torch, torch.int32),
+       kept_pages=c["kept_pages"], page=c["page"], max_position=mp, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+
+
+def test_refused_beyond_max_position():
+    """A row past the launch's stated max_position (which sized the key split) is
+    refused rather than read with part of its keys dropped."""
+    from tessera_amd import abi
+    from tessera_amd import rules as R
+    c = paged_case(61, [500, 500])
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    got = from_dev(R.attend_rows(to_dev(c["q"], torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                                 to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                                 keys=c["keys"], scale=0.1, table=to_dev(c["table"], torch, torch.int32),
+                                 kept_pages=c["kept_pages"], page=c["page"], max_position=200, status=status))
+    torch.cuda.synchronize()
+    assert int(status.item()) == abi.TS_STATUS_POSITION
+    assert np.all(np.isnan(got))
