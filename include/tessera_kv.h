@@ -87,6 +87,35 @@ int tessera_kv_consistent(const ts_kv_pool *p);
 uint64_t tessera_kv_error_value(const ts_kv_pool *p);
 uint64_t tessera_kv_error_value2(const ts_kv_pool *p);
 
+/* ----------------------------------------------------------------------------
+ * Device side: the copies Pool::grow asks for, made on the GPU.
+ * ------------------------------------------------------------------------- */
+
+/* Status bit (ORed into ts_kv_copy_args.status): a copy named a page >= pages, more
+ * rows than a page, a page onto itself, or a buffer not 16-byte aligned; it was
+ * skipped. */
+#define TS_KV_STATUS_COPY 2u
+
+typedef struct {
+    void *const *buffers;      /* device array [buffer_count] of kept-row buffers (e.g. K and V of each layer),
+                                  each [pages * page, row_bytes] */
+    const ts_kv_copy *copies;  /* device array [copy_count], as Pool::grow returned them */
+    uint32_t buffer_count, copy_count;
+    uint32_t page;             /* rows per page */
+    uint32_t row_bytes;        /* bytes of one kept row (kv_heads * width * 2 for bf16), a multiple of 16 */
+    uint32_t pages;            /* pages each buffer holds */
+    uint32_t *status;          /* device word or NULL */
+} ts_kv_copy_args;
+
+/* Rows [0, rows) of page `from` to page `to` in every buffer, for every copy, stream
+ * ordered before the launch that appends (one launch, no host round trip; graph
+ * capturable). Copies of one call must not overlap each other's pages.
+ * Replaces: the "make the copies before the launch" step of Pool::grow
+ * (engine/ir/kv/src/pool.rs:193-223); the reference's engine refuses grows that need
+ * a copy (engine/engine/src/kept.rs:127-141) and uploads only the table
+ * (engine/engine/src/lanes.rs:60-66). */
+int tessera_hip_kv_copy(const ts_kv_copy_args *a, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

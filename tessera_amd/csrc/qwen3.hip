@@ -88,6 +88,8 @@ struct ts_qwen3 {
     uint32_t *d_tok, *d_pos, *d_slot, *d_hist, *d_prompt, *d_prompt_pos, *d_prompt_slot, *d_table;
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    void **d_buffers = nullptr;  // the K and V kept-row buffers of every layer (page copies)
+    ts_kv_copy *d_copy = nullptr;
     ts_kv_pool *pool = nullptr;
     ts_kv_run run{0, 0};
     bool have_run = false;
@@ -344,8 +346,16 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
         (rc = m->alloc(&m->d_tok, 1)) || (rc = m->alloc(&m->d_pos, 1)) || (rc = m->alloc(&m->d_slot, 1)) ||
         (rc = m->alloc(&m->d_hist, (size_t)c.max_context + 1)) || (rc = m->alloc(&m->d_prompt, R)) ||
         (rc = m->alloc(&m->d_prompt_pos, R)) || (rc = m->alloc(&m->d_prompt_slot, R)) ||
-        (rc = m->alloc(&m->d_table, m->kept_pages)) || (rc = m->alloc(&m->rope, (size_t)c.max_context * D)))
+        (rc = m->alloc(&m->d_table, m->kept_pages)) || (rc = m->alloc(&m->rope, (size_t)c.max_context * D)) ||
+        (rc = m->alloc(&m->d_buffers, 2 * (size_t)c.layers)) || (rc = m->alloc(&m->d_copy, 1)))
         return fail(rc);
+    {
+        std::vector<void *> bufs;
+        for (const Layer &L : m->layers) { bufs.push_back(L.k_cache); bufs.push_back(L.v_cache); }
+        e = hipMemcpyAsync(m->d_buffers, bufs.data(), bufs.size() * sizeof(void *), hipMemcpyHostToDevice, m->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) return fail(ts::hip_status(e, "buffer list upload"));
+    }
     if ((rc = tessera_hip_rope_table(m->rope, c.max_context, D, c.theta, m->stream))) return fail(rc);
     m->ws_bytes = workspace_need(m);
     if (m->ws_bytes) {
@@ -425,6 +435,22 @@ extern "C" int tessera_qwen3_read(ts_qwen3 *m, const char *name, uint32_t layer,
     return TS_OK;
 }
 
+namespace {
+
+// The copy Pool::grow asked for, made in every layer's K and V before anything
+// appends (engine/ir/kv/src/pool.rs:193-223).
+int copy_pages(ts_qwen3 *m, const ts_kv_copy &cp) {
+    hipError_t e = hipMemcpyAsync(m->d_copy, &cp, sizeof cp, hipMemcpyHostToDevice, m->stream);
+    if (e != hipSuccess) return ts::hip_status(e, "page copy upload");
+    ts_kv_copy_args a;
+    memset(&a, 0, sizeof a);
+    a.buffers = m->d_buffers; a.copies = m->d_copy; a.buffer_count = 2 * m->c.layers; a.copy_count = 1;
+    a.page = m->c.page; a.row_bytes = m->c.kv_heads * m->c.head_dim * 2; a.pages = m->total_pages;
+    return tessera_hip_kv_copy(&a, m->stream);
+}
+
+}  // namespace
+
 extern "C" int tessera_qwen3_prefill(ts_qwen3 *m, const uint32_t *tokens, uint32_t count, uint32_t *next) {
     TS_REQUIRE(m && tokens && count >= 1, "qwen3_prefill: empty prompt");
     TS_REQUIRE(count <= m->c.max_prompt, "qwen3_prefill: %u tokens (at most %u)", count, m->c.max_prompt);
@@ -440,6 +466,7 @@ extern "C" int tessera_qwen3_prefill(ts_qwen3 *m, const uint32_t *tokens, uint32
     uint32_t ncp = 0;
     k = tessera_kv_grow(m->pool, m->run, m->c.max_context, &cp, &ncp);
     if (k != TS_KV_OK) return ts::fail(TS_ERR_ARG, "qwen3_prefill: page pool refused growth (%d)", k);
+    if (ncp) TRY(copy_pages(m, cp));
     const uint32_t *pages = nullptr;
     uint32_t npages = 0;
     tessera_kv_pages(m->pool, m->run, &pages, &npages);

@@ -36,6 +36,16 @@ class PageCopy(C.Structure):
         return (self.from_, self.to, self.rows)
 
 
+class CopyArgs(C.Structure):
+    """ts_kv_copy_args (include/tessera_kv.h)."""
+    _fields_ = [("buffers", C.c_void_p), ("copies", C.c_void_p), ("buffer_count", C.c_uint32),
+                ("copy_count", C.c_uint32), ("page", C.c_uint32), ("row_bytes", C.c_uint32),
+                ("pages", C.c_uint32), ("status", C.c_void_p)]
+
+
+STATUS_COPY = 2  # TS_KV_STATUS_COPY
+
+
 class Stats(C.Structure):
     _fields_ = [("size", C.c_uint64), ("active", C.c_uint64), ("worst", C.c_uint64),
                 ("live_runs", C.c_uint64), ("kept_runs", C.c_uint64)]
@@ -72,6 +82,7 @@ SIGNATURES = {
     "tessera_kv_consistent": (C.c_int, [_P]),
     "tessera_kv_error_value": (C.c_uint64, [_P]),
     "tessera_kv_error_value2": (C.c_uint64, [_P]),
+    "tessera_hip_kv_copy": (C.c_int, [C.POINTER(CopyArgs), _P]),
 }
 
 _bound = False
@@ -162,3 +173,23 @@ class Pool:
 
     def consistent(self):
         return bool(self._l.tessera_kv_consistent(self._p))
+
+
+def copy_pages(buffers, copies, *, page, pages, status=None):
+    """Makes Pool.grow's copies on the device in every kept-row buffer (torch tensors
+    [pages * page, ...], e.g. K and V of each layer), in stream order before the
+    launch that appends. copies: [(from, to, rows), ...]."""
+    import torch
+    if not copies:
+        return
+    dev = buffers[0].device
+    ptrs = torch.tensor([b.data_ptr() for b in buffers], dtype=torch.int64).to(dev)
+    raw = torch.tensor([[f, t, r & 0xFFFFFFFF, r >> 32] for f, t, r in copies], dtype=torch.int64)
+    cps = raw.to(torch.int32).to(dev)  # ts_kv_copy: u32 from, u32 to, u64 rows (little endian)
+    a = CopyArgs()
+    a.buffers, a.copies = ptrs.data_ptr(), cps.data_ptr()
+    a.buffer_count, a.copy_count, a.page, a.pages = len(buffers), len(copies), page, pages
+    a.row_bytes = buffers[0][0].numel() * buffers[0].element_size()
+    a.status = status.data_ptr() if status is not None else None
+    rc = lib().tessera_hip_kv_copy(C.byref(a), C.c_void_p(torch.cuda.current_stream().cuda_stream))
+    abi.check(rc, "tessera_hip_kv_copy")
