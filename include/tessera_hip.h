@@ -188,6 +188,18 @@ typedef struct {
 int tessera_hip_attend_rows(const ts_rows_args *a, void *stream);
 size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
 
+/* attend_rows with no workspace and no allocation: the split-KV partials live in a
+ * fixed device array of tessera_hip_attend_rows_noalloc_limit() bytes (16 MiB; one
+ * copy per GPU, held until the process ends). a->workspace is ignored. Launches whose
+ * partials would pass the limit (rows * kv_heads * partitions * heads/kv_heads * 520
+ * bytes; e.g. 32 rows at 8192 keys need 8.5 MB) fail with TS_ERR_WORKSPACE. Calls
+ * on one GPU share the array: calls that overlap in time on that GPU (different
+ * streams) race; stream-ordered calls do not.
+ * No counterpart in the reference: for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int tessera_hip_attend_rows_noalloc(const ts_rows_args *a, void *stream);
+size_t tessera_hip_attend_rows_noalloc_limit(void);
+
 /* The decode step of a Qwen3 layer in one launch: per-head RmsNorm (q_gain /
  * k_gain, eps) and Halves RoPE (angles from rope_table, rows >= max_position + 1,
  * as tessera_hip_rope_table fills it) of q and of the new k from the raw q/k/v

@@ -90,6 +90,8 @@ SIGNATURES = {
     "tessera_hip_mix": (C.c_int, [_P, _P, _P, _U, _U, _U, _P]),
     "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
+    "tessera_hip_attend_rows_noalloc": (C.c_int, [_RA, _P]),
+    "tessera_hip_attend_rows_noalloc_limit": (C.c_size_t, []),
     "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_step": (C.c_int, [_RA, _P, _P, _P, _P, _U, C.c_float, _P]),
     "tessera_hip_rope_table": (C.c_int, [_P, _U, _U, C.c_float, _P]),

@@ -29,6 +29,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -781,4 +782,62 @@ extern "C" int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, 
     memset(&p, 0, sizeof p);
     p.qkv = qkv; p.q_gain = q_gain; p.k_gain = k_gain; p.rope = rope_table; p.eps = eps;
     return launch_rows<true>(&b, p, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The entry point that allocates nothing: split-KV partials in a fixed device
+// array instead of a caller's workspace.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = size_t(16) << 20;  // partials of up to 16 MiB per launch
+constexpr int kMaxDevices = 64;
+
+// One copy per GPU the library runs on, held until the process ends. In host code
+// this name is only a stand-in: its device address comes from hipGetSymbolAddress.
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex scratch_mu;
+void *scratch_at[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device with that
+// device current.
+int scratch_ptr(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return ts::hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return ts::fail(TS_ERR_ARG, "attend_rows_noalloc: device %d", dev);
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (!scratch_at[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return ts::hip_status(e, "hipGetSymbolAddress(scratch)");
+        scratch_at[dev] = p;
+    }
+    *out = scratch_at[dev];
+    return TS_OK;
+}
+
+}  // namespace
+
+extern "C" size_t tessera_hip_attend_rows_noalloc_limit(void) { return kScratchBytes; }
+
+extern "C" int tessera_hip_attend_rows_noalloc(const ts_rows_args *a, void *stream) {
+    int rc = check(a);
+    if (rc) return rc;
+    if (a->rows == 0) return TS_OK;
+    const size_t need = partials_bytes(a, split(a, false));
+    if (need > kScratchBytes)
+        return ts::fail(TS_ERR_WORKSPACE,
+                        "attend_rows_noalloc: %zu bytes of partials needed, the fixed scratch holds %zu "
+                        "(fewer rows or a shorter max_position; or tessera_hip_attend_rows with a workspace)",
+                        need, kScratchBytes);
+    void *ptr = nullptr;
+    if ((rc = scratch_ptr(&ptr))) return rc;
+    ts_rows_args b = *a;
+    b.workspace = ptr;  // the partials are written in full before the merge reads them: no clearing
+    b.workspace_bytes = kScratchBytes;
+    RowsParams p;
+    memset(&p, 0, sizeof p);
+    return launch_rows<false>(&b, p, stream);
 }
