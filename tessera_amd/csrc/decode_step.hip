@@ -9,34 +9,30 @@
 // arithmetic of every stage is the one of the kernels it replaces (gemv.hip,
 // attention.hip, rows.hip): f32 activations, bf16 weights widened exactly, f32 sums.
 //
-// Why one launch. At batch 1 every product only streams its weights (31 MB per
-// layer), and a graph of 5 kernels per layer spends ~31 us per layer in per-kernel
-// ramp and drain against ~4 us of HBM time. Here one group per CU lives for the
-// whole decode call and:
-//  * a group owns fixed rows of every matrix (ceil(N / groups) rows);
-//  * two DMA waves stream those rows, phase after phase and layer after layer,
-//    straight into a 128 KiB LDS ring with global_load_lds (no registers), up to a
-//    ring ahead of the compute, so HBM stays busy while the compute waits for the
-//    previous phase's activations;
-//  * six compute waves hand activations between phases through "tagged" words in
-//    HBM: each output value is one 8-byte store of (f32 value, u32 epoch) at agent
-//    scope (coherent across XCDs), and a consumer polls the words it needs until
-//    every epoch matches. The data is its own flag: no counters, no fences, no
-//    cache write-back, one memory round trip per hand-off;
-//  * all eight waves meet at hardware barriers. The DMA waves walk the same
-//    schedule of barriers as the compute waves: before the barrier that starts a
-//    phase they wait (vmcnt) for that phase's rows, after the barrier that ends it
-//    they reuse its ring slots. Ring occupancy is known, never signalled;
-//  * the first q_heads groups also run the attention of one q head each, with
-//    the kept rows of earlier positions loaded before the q/k/v hand-off arrives;
-//  * the lm_head rows stream through the same ring in chunks; every group publishes
-//    its (max, index), and every group reduces all of them, so the next step's
-//    token needs no extra hand-off.
-// Waits are bounded: a poll that passes 2 s (100 MHz clock) sets the error word;
-// every poll also watches that word, and a failed poll lets its group run on
-// without waiting, so the grid always reaches its last barrier and ends. Groups
-// are launched cooperatively (all resident), one per CU.
+// Why one launch, and why roles. At batch 1 every product only streams its weights
+// (31 MB a layer, ~4 us of HBM time), while each stage needs the whole output of the
+// one before: the step is a chain of ~140 chip-wide hand-offs, and their latency,
+// not HBM, sets its speed. A hand-off among all 256 CUs measured ~2.2 us on MI355X,
+// among 32 ~1.3 us. So each group (one per CU, resident for the whole call) has one
+// role for the whole launch:
+//  * qkv, o, gate/up or down: the group owns fixed rows of that matrix in every
+//    layer and keeps them in registers (<= 72 VGPRs a lane). Right after a layer's
+//    products it issues the loads of the next layer's rows into the same registers,
+//    so they land during the ~10 us until that layer comes round: no weight latency
+//    on the chain, and each hand-off runs between two role sets of 32..96 groups;
+//  * attention: one group per kv head runs both q heads of its pair (the new k/v
+//    row is appended and later read by the same group: no cross-CU ordering);
+//  * every group then streams its rows of the tied lm_head; every group publishes
+//    its (max, index), and the groups that need the token reduce all of them.
+// Hand-offs are "tagged" words in HBM: each value is one 8-byte store of (f32 value,
+// u32 epoch) at agent scope (coherent across XCDs), and a consumer polls the words it
+// needs until every epoch matches: the data is its own flag. Waits are bounded: a
+// poll that passes 2 s (100 MHz clock) sets the error word; every poll also watches
+// that word, and a failed poll lets its group run on without waiting, so the grid
+// always ends. Groups are launched cooperatively (all resident), one per CU.
 #include <string.h>
+
+#include <algorithm>
 
 #include "common.h"
 #include "decode_step.h"
@@ -44,91 +40,60 @@
 namespace ts {
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-constexpr uint32_t kCW = 6;                    // compute waves
-constexpr uint32_t kDW = 2;                    // DMA waves
-constexpr uint32_t kCT = kCW * 64;             // compute threads
-constexpr uint32_t kThreads = (kCW + kDW) * 64;
-constexpr uint32_t kRing = 128;                // ring units of 1 KiB
-constexpr uint32_t kMaxOut = 56;               // DMA loads in flight per wave (vmcnt holds 63)
-constexpr uint32_t kBurst = 8;                 // DMA loads a wave issues per barrier
-constexpr uint32_t kLmBurst = 24;              // the same in the lm_head chunks (7 us a token over 8)
-constexpr uint32_t kRW = 4;                    // product rows per compute wave
-constexpr uint32_t kChunk = kRW * kCW;         // lm_head rows per chunk
-constexpr uint32_t kMaxXa = 3072;              // staged input floats (H, Hq*128 and F)
-constexpr uint32_t kMaxH = 1024;
+constexpr uint32_t kW = 8;                      // waves per group
+constexpr uint32_t kT = kW * 64;                // threads per group
+constexpr uint32_t kMaxH = 1024;                // hidden (2 chunks of 8 per lane)
+constexpr uint32_t kMaxQD = 2048;               // q heads x 128 (4 chunks per lane)
+constexpr uint32_t kMaxF = 3072;                // ffn (6 chunks per lane)
 constexpr uint32_t kMaxPages = 512;
-constexpr uint64_t kTimeout = 200000000ull;    // 2 s of the 100 MHz clock
-constexpr int kNX = (kMaxXa + kCT - 1) / kCT;  // staged words per compute thread (widest input)
-constexpr int kNH = (kMaxH + kCT - 1) / kCT;   // staged words per compute thread (hidden-wide input)
-constexpr uint32_t kMaxGroups = 448;           // groups the step supports (2 pick words each)
-constexpr int kNA = (2 * kMaxGroups + kCT - 1) / kCT;
-constexpr int kPre = 7;                        // 4-key blocks per wave loaded before q arrives
-static_assert(kCW >= 4 && kCW <= 8, "attention uses waves 0..3 and LDS partials for up to 8 waves");
+constexpr uint32_t kLdsBytes = 96 * 1024;       // more than half the CU's LDS: one group per CU
+constexpr uint64_t kTimeout = 200000000ull;     // 2 s of the 100 MHz clock
+constexpr int kPre = 5;                         // 4-key blocks per wave per attention pass
+constexpr uint32_t kMaxLm = 1024;               // lm_head rows a group holds
+constexpr int kLmDepth = 4;                     // lm_head row tiles in flight per wave
+// 16-row tiles a group holds per product role (gate/up: gate tiles then up tiles).
+constexpr int kTilesQkv = 4, kTilesO = 2, kTilesGu = 4, kTilesDn = 2;
+
+enum Role : uint32_t { kQkv = 0, kO = 1, kGu = 2, kDn = 3, kAtt = 4 };
 
 // LDS layout (bytes).
-constexpr uint32_t kRingOff = 0;
-constexpr uint32_t kXaOff = kRingOff + kRing * 1024;
-constexpr uint32_t kXrOff = kXaOff + kMaxXa * 4;
-constexpr uint32_t kRedOff = kXrOff + kMaxH * 4;
-constexpr uint32_t kTblOff = kRedOff + 1024 * 4;
-constexpr uint32_t kSsqOff = kTblOff + kMaxPages * 4;
-constexpr uint32_t kCtlOff = kSsqOff + 16 * 4;
-constexpr uint32_t kLdsBytes = kCtlOff + 16 * 4;
+constexpr uint32_t kXsOff = 0;                            // staged inputs, 3 bf16 parts [2][3][kMaxF]
+constexpr uint32_t kResOff = kXsOff + 2 * 3 * kMaxF * 2;  // residual rows [2][64]
+constexpr uint32_t kSsqOff = kResOff + 2 * 64 * 4;        // sums of squares [2][kW]
+constexpr uint32_t kPartOff = kSsqOff + 2 * kW * 4;       // per-wave row partials [2][kW][64]
+constexpr uint32_t kLmPartOff = kPartOff + 2 * kW * 64 * 4;  // lm_head row partials [kW][kMaxLm]
+constexpr uint32_t kTblOff = kLmPartOff + kW * kMaxLm * 4;  // page table [kMaxPages]
+constexpr uint32_t kAttOff = kTblOff + kMaxPages * 4;     // attention scratch
+constexpr uint32_t kAttBytes = 512 * 4 + 2 * 128 * 4 + 2 * 128 * 2 + 2 * kW * 2 * 4 + 2 * kW * 128 * 4;
+constexpr uint32_t kBestOff = kAttOff + kAttBytes;        // per-wave (max, index) [kW][2]
+constexpr uint32_t kPickOff = kBestOff + kW * 2 * 4;      // every group's (max, index) [2 * groups]
+constexpr uint32_t kCtlOff = kPickOff + 2 * kStepMaxGroups * 4;
+constexpr uint32_t kLdsUsed = kCtlOff + 16 * 4;
+static_assert(kLdsUsed <= kLdsBytes, "LDS layout");
 // Control words.
 constexpr uint32_t kAbort = 0;  // a wait of this group gave up
 constexpr uint32_t kTok = 1;    // the step's token
 
-TS_DEV uint32_t units(uint32_t bytes) { return (bytes + 1023) >> 10; }
-
-// Rows [first, first + count) of N split over NG groups, ceil(N / NG) each.
+// Rows [first, first + count) of N split over n parts, ceil(N / n) each.
 struct Split {
     uint32_t first, count;
 };
-TS_DEV Split split(uint32_t n, uint32_t ng, uint32_t g) {
-    const uint32_t per = (n + ng - 1) / ng;
-    const uint32_t f = min(n, g * per);
-    return {f, min(n, f + per) - f};
+__host__ __device__ inline Split split(uint32_t n, uint32_t parts, uint32_t i) {
+    const uint32_t per = (n + parts - 1) / parts;
+    const uint32_t f = i * per < n ? i * per : n;
+    return {f, (f + per < n ? f + per : n) - f};
 }
 
-// This group's rows of every matrix, and the stream units they take.
-struct Plan {
-    Split q, o, f, v;  // qkv rows, o/down rows, gate (and up) rows, lm_head rows
-    uint32_t uq, uo, ug, ud, layer, chunks, step;
-    uint32_t QKV, QD;
-};
-TS_DEV uint32_t chunk_units(const DecodeStepArgs &p, const Plan &pl, uint32_t c) {
-    return units(min(kChunk, pl.v.count - c * kChunk) * p.H * 2);
-}
-TS_DEV Plan plan(const DecodeStepArgs &p, uint32_t g) {
-    Plan pl;
-    pl.QD = p.Hq * 128;
-    pl.QKV = (p.Hq + 2 * p.Hkv) * 128;
-    pl.q = split(pl.QKV, p.NG, g);
-    pl.o = split(p.H, p.NG, g);
-    pl.f = split(p.F, p.NG, g);
-    pl.v = split(p.V, p.NG, g);
-    pl.uq = units(pl.q.count * p.H * 2);
-    pl.uo = units(pl.o.count * pl.QD * 2);
-    pl.ug = units(pl.f.count * p.H * 2);
-    pl.ud = units(pl.o.count * p.F * 2);
-    pl.layer = pl.uq + pl.uo + 2 * pl.ug + pl.ud;
-    pl.chunks = (pl.v.count + kChunk - 1) / kChunk;
-    pl.step = p.L * pl.layer;
-    for (uint32_t c = 0; c < pl.chunks; c++) pl.step += chunk_units(p, pl, c);
-    return pl;
-}
-
-// Hand-off word offsets: per layer qkv, attention, x after o, silu*up, x after down.
+// Hand-off word offsets: per layer qkv, attention, x after o, silu*up, x after down;
+// then two words per group for the greedy pick.
 struct Hand {
     uint32_t qkv, att, x2, hf, xo, block, am;
 };
-TS_DEV Hand hand(const DecodeStepArgs &p, const Plan &pl) {
+TS_DEV Hand hand(const DecodeStepArgs &p) {
     Hand h;
     h.qkv = 0;
-    h.att = pl.QKV;
-    h.x2 = h.att + pl.QD;
+    h.att = (p.Hq + 2 * p.Hkv) * 128;
+    h.x2 = h.att + p.Hq * 128;
     h.hf = h.x2 + p.H;
     h.xo = h.hf + p.F;
     h.block = h.xo + p.H;
@@ -142,18 +107,48 @@ TS_DEV void st_tag(uint64_t *p, uint32_t bits, uint32_t tag) {
 }
 TS_DEV uint64_t now() { return __builtin_amdgcn_s_memrealtime(); }
 
-// A barrier of all eight waves that also publishes this wave's LDS writes; global
-// loads stay in flight (__syncthreads would wait for them).
+// A wave-uniform address as a scalar value (a load then takes it as its scalar base and
+// only the lane's offset in a vector register).
+TS_DEV const char *uniform(const void *ptr) {
+    const uint64_t v = (uint64_t)ptr;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const char *)(((uint64_t)hi << 32) | lo);
+}
+
+// A barrier of the group's waves that publishes their LDS writes; global loads stay
+// in flight (__syncthreads would wait for them, draining the weight prefetch).
 TS_DEV void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 struct Ctx {
     char *lds;
-    float *xa, *xr, *red, *ssq;
-    uint32_t *tbl;
     volatile uint32_t *ctl;
     uint32_t *err;
-    uint32_t tid, wave, lane;
+    uint32_t *tbl;
+    uint32_t tid, wave, lane, g;
+    uint32_t ph;  // staging parity
+    TS_DEV uint16_t *xs() const { return (uint16_t *)(lds + kXsOff) + (ph & 1) * 3 * kMaxF; }
+    TS_DEV float *res() const { return (float *)(lds + kResOff) + (ph & 1) * 64; }
+    TS_DEV float *ssq() const { return (float *)(lds + kSsqOff) + (ph & 1) * kW; }
+    TS_DEV float *part() const { return (float *)(lds + kPartOff) + (ph & 1) * kW * 64; }
 };
+
+// Sums (maxima) over the four 16-lane rows of a wave, in every lane.
+TS_DEV float rows4_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+TS_DEV float rows4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+// Whole-wave total in every lane on the VALU alone: DPP within rows of 16, then the
+// gfx950 permlane swaps across rows (no LDS round trips, unlike a shuffle).
+TS_DEV float wave_total(float v) { return rows4_sum(row16_sum(v)); }
 
 // One step of a bounded wait; false ends the wait (timed out here, or anywhere).
 TS_DEV bool spin(Ctx &c, uint32_t &it, uint64_t &t0) {
@@ -177,152 +172,419 @@ TS_DEV bool spin(Ctx &c, uint32_t &it, uint64_t &t0) {
     return true;
 }
 
-// Tagged words src[tid + kCT k] (k < NX, index < n) into v[k]: every load is
-// issued, then the loads whose epoch is stale are reissued until none is. (A
-// second round of loads kept in flight measured slower: it doubles the polling
-// traffic every group puts on the memory system.)
+// Tagged words src[tid + kT k] (k < NX, index < n) into v[k], and (extra non-null)
+// one more word into *xv: every load is issued, then the loads whose epoch is stale
+// are reissued until none is.
 template <int NX>
-TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[NX]) {
-    uint64_t w[NX];
+TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[NX],
+                 const uint64_t *extra = nullptr, float *xv = nullptr) {
+    uint64_t w[NX], x;
 #pragma unroll
     for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kCT * k;
+        const uint32_t i = c.tid + kT * k;
         w[k] = i < n ? ld_tag(src + i) : ((uint64_t)tag << 32);
     }
+    x = extra ? ld_tag(extra) : ((uint64_t)tag << 32);
     uint64_t t0 = 0;
     uint32_t it = 0;
     for (;;) {
-        bool ready = true;
+        bool ready = (uint32_t)(x >> 32) == tag;
 #pragma unroll
         for (int k = 0; k < NX; k++) ready &= (uint32_t)(w[k] >> 32) == tag;
         if (ready || !spin(c, it, t0)) break;
 #pragma unroll
         for (int k = 0; k < NX; k++)
-            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(src + c.tid + kCT * k);
+            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(src + c.tid + kT * k);
+        if ((uint32_t)(x >> 32) != tag) x = ld_tag(extra);
     }
 #pragma unroll
     for (int k = 0; k < NX; k++) v[k] = __uint_as_float((uint32_t)w[k]);
+    if (extra) *xv = __uint_as_float((uint32_t)x);
 }
 
-TS_DEV float dot8(u32x4 w, float4 a, float4 b, float acc) {
-    acc += a.x * lo_bf16(w.x);
-    acc += a.y * hi_bf16(w.x);
-    acc += a.z * lo_bf16(w.y);
-    acc += a.w * hi_bf16(w.y);
-    acc += b.x * lo_bf16(w.z);
-    acc += b.y * hi_bf16(w.z);
-    acc += b.z * lo_bf16(w.w);
-    acc += b.w * hi_bf16(w.w);
-    return acc;
+// One tagged word (thread-private wait).
+TS_DEV float poll1(Ctx &c, const uint64_t *src, uint32_t tag) {
+    uint64_t w = ld_tag(src);
+    uint64_t t0 = 0;
+    uint32_t it = 0;
+    while ((uint32_t)(w >> 32) != tag && spin(c, it, t0)) w = ld_tag(src);
+    return __uint_as_float((uint32_t)w);
 }
 
-TS_DEV const u32x4 *ring_at(const char *lds, uint32_t u0, uint32_t byte) {
-    const uint32_t u = u0 + (byte >> 10);
-    return (const u32x4 *)(lds + kRingOff + ((u & (kRing - 1)) << 10) + (byte & 1023));
-}
-
-// Partial dot products of NR rows of this wave with xa[0, K), over pieces [j0, j1)
-// of 8 values: every LDS read of an iteration is issued before its math.
-template <int NR>
-TS_DEV void dots(const Ctx &c, const uint32_t (&u0)[kRW], const uint32_t (&rr)[kRW], uint32_t j0, uint32_t j1,
-                 float (&acc)[kRW]) {
-    const float4 *x4 = (const float4 *)c.xa;
-#pragma unroll 2
-    for (uint32_t j = j0 + c.lane; j < j1; j += 64) {
-        const float4 a = x4[2 * j], b = x4[2 * j + 1];
-        u32x4 w[NR];
-#pragma unroll
-        for (int i = 0; i < NR; i++) w[i] = *ring_at(c.lds, u0[i], rr[i] + j * 16);
-#pragma unroll
-        for (int i = 0; i < NR; i++) acc[i] = dot8(w[i], a, b, acc[i]);
-    }
-}
-
-// Partial dot products of R rows (R <= kRW kCW) with xa[0, K): rows r < Ra are rows
-// of the stream segment at unit ua, rows r >= Ra rows r - Ra of the segment at ub.
-// With R >= kCW wave w owns rows w + kCW i; fewer rows split k across S = kCW / R
-// waves. Row r's value is the sum over s < S of red[r * S + s] (in that order).
-TS_DEV uint32_t gemv_part(Ctx &c, uint32_t ua, uint32_t Ra, uint32_t ub, uint32_t R, uint32_t K, float *red) {
-    if (R == 0) return 1;
-    const uint32_t P = K >> 3, rowb = K * 2;
-    const uint32_t S = R >= kCW ? 1 : kCW / R;
-    uint32_t u0[kRW], rr[kRW], nr, j0 = 0, j1 = P;
-    float acc[kRW];
-    if (S > 1) {
-        nr = c.wave < R * S ? 1 : 0;
-        const uint32_t r = min(c.wave / S, R - 1), s = c.wave % S, per = (P + S - 1) / S;
-        j0 = min(P, s * per);
-        j1 = min(P, j0 + per);
-#pragma unroll
-        for (int i = 0; i < kRW; i++) {
-            u0[i] = r < Ra ? ua : ub;
-            rr[i] = (r < Ra ? r : r - Ra) * rowb;
-        }
-    } else {
-        nr = c.wave < R ? (R - c.wave + kCW - 1) / kCW : 0;
-#pragma unroll
-        for (int i = 0; i < kRW; i++) {
-            const uint32_t r = min(c.wave + kCW * i, R - 1);
-            u0[i] = r < Ra ? ua : ub;
-            rr[i] = (r < Ra ? r : r - Ra) * rowb;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < kRW; i++) acc[i] = 0.0f;
-    switch (nr) {  // uniform across the wave
-    case 1: dots<1>(c, u0, rr, j0, j1, acc); break;
-    case 2: dots<2>(c, u0, rr, j0, j1, acc); break;
-    case 3: dots<3>(c, u0, rr, j0, j1, acc); break;
-    case 4: dots<4>(c, u0, rr, j0, j1, acc); break;
-    default: break;
-    }
-#pragma unroll
-    for (int i = 0; i < kRW; i++) {
-        if ((uint32_t)i < nr) {
-            const float t = wave_sum(acc[i]);
-            if (c.lane == 0) red[c.wave + kCW * i] = t;
-        }
-    }
-    return S;
-}
-
-TS_DEV float row_value(const float *red, uint32_t r, uint32_t S) {
-    float v = 0.0f;
-    for (uint32_t s = 0; s < S; s++) v += red[r * S + s];
-    return v;
-}
-
-// Stage an input vector of n <= 3072 values: xa[i] = v * g[i], xr[i] = v when
-// keep_raw, and the partial sums of squares of the RmsNorm; read back after the
-// next barrier by norm_inv.
+// Gains of the words this thread stages (1 without a gain), loaded before the poll.
 template <int NX>
-TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX], bool keep_raw) {
-    float ss = 0.0f;
+TS_DEV void gains(const Ctx &c, const float *g, uint32_t n, float (&gv)[NX]) {
 #pragma unroll
     for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kCT * k;
+        const uint32_t i = c.tid + kT * k;
+        gv[k] = g && i < n ? g[i] : 1.0f;
+    }
+}
+
+// Stage an input of n values: x = v * g (the preloaded gains) as three bf16 parts,
+// x = hi + mid + lo (8 + 8 + 8 mantissa bits: exact for normal values), the B
+// operand columns of the matrix-unit products; and the group's partial sums of
+// squares of v (read after the next barrier by norm_inv).
+template <int NX>
+TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX]) {
+    float ss = 0.0f;
+    uint16_t *xs = c.xs();
+#pragma unroll
+    for (int k = 0; k < NX; k++) {
+        const uint32_t i = c.tid + kT * k;
         if (i < n) {
-            c.xa[i] = v[k] * g[k];
-            if (keep_raw) c.xr[i] = v[k];
+            const float x = v[k] * g[k];
+            const uint16_t hi = bf16_bits(x);
+            const float r1 = x - bf16_float(hi);
+            const uint16_t mid = bf16_bits(r1);
+            xs[i] = hi;
+            xs[kMaxF + i] = mid;
+            xs[2 * kMaxF + i] = bf16_bits(r1 - bf16_float(mid));
             ss += v[k] * v[k];
         }
     }
-    ss = wave_sum(ss);
-    if (c.lane == 0) c.ssq[c.wave] = ss;
+    ss = wave_total(ss);
+    if (c.lane == 0) c.ssq()[c.wave] = ss;
 }
 
 // 1/sqrt(mean(v^2) + eps): the RmsNorm scale, folded into the products' results
 // (sum_k (x_k inv g_k) w_k = inv sum_k (x_k g_k) w_k).
 TS_DEV float norm_inv(const Ctx &c, uint32_t n, float eps) {
     float t = 0.0f;
-    for (uint32_t w = 0; w < kCW; w++) t += c.ssq[w];
+    for (uint32_t w = 0; w < kW; w++) t += c.ssq()[w];
     return 1.0f / sqrtf(t / (float)n + eps);
+}
+
+// Optional phase stamps of the first step (thread 0 of every group): row l, slot k.
+TS_DEV void mark(const DecodeStepArgs &p, const Ctx &c, uint32_t t, uint32_t l, uint32_t k) {
+    if (p.marks && t == 0 && c.tid == 0) {
+        p.marks[((size_t)c.g * (p.L + 2) + l) * 10 + k] = now();
+    }
+}
+
+TS_DEV void better(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+// 16-row tiles of lm_head rows per group (every group the same count; rows past a
+// group's share are zeros in the packed copy).
+__host__ __device__ inline uint32_t lm_tiles(uint32_t V, uint32_t NG) { return ((V + NG - 1) / NG + 15) / 16; }
+
+// ---------------------------------------------------------------------------
+// Products on the matrix unit. A 16-row tile of weights is the A operand of
+// v_mfma_f32_16x16x32_bf16 (lane l: row l % 16, k 8 (l / 16) .. +8 of a 32-deep
+// k-step); the input is the B operand with three live columns, its three bf16
+// parts (x = hi + mid + lo, exact): columns 0, 1, 2 hold them, the rest zero. Lane l
+// of the result holds column l % 16, rows 4 (l / 16) .. +3, so rows' sums are
+// columns 0 + 1 + 2: lanes 0, 16, 32, 48 after two DPP swaps. A wave owns
+// a range of k-steps of every tile; the waves' partials meet in LDS and are summed
+// in wave order.
+// ---------------------------------------------------------------------------
+
+// B fragment of k-step ks from the staged input: column 0 the high parts of k values
+// ks * 32 + 8 (l / 16) .. +8, column 1 the middle, column 2 the low, the rest zero.
+TS_DEV u32x4 x_frag(const Ctx &c, const uint16_t *xs, uint32_t ks, uint32_t K) {
+    const uint32_t col = c.lane & 15, k0 = ks * 32 + (c.lane >> 4) * 8;
+    if (col >= 3 || k0 >= K) return u32x4{0, 0, 0, 0};
+    return *(const u32x4 *)&xs[col * kMaxF + k0];
+}
+
+// The tile's row sums (columns 0 + 1 + 2) into part[t * 16 + row] from lanes 0, 16,
+// 32, 48.
+TS_DEV void tile_out(const Ctx &c, f32x4 acc, float *part, uint32_t t) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float a = acc[i] + dpp_f(acc[i], 0);  // columns 0 + 1 (and 2 + 3 in lane 2)
+        v[i] = a + dpp_f(a, 1);                     // + columns 2 + 3 (3 is zero)
+    }
+    if ((c.lane & 15) == 0) {
+        float *dst = part + t * 16 + 4 * (c.lane >> 4);
+        *(float4 *)dst = make_float4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The lm_head rows of this group and the group's best (value, index), published.
+// Wave w streams k-steps [4 w, 4 w + 4) of every 16-row tile, kLmDepth tiles in
+// flight; the row sums meet in LDS.
+// ---------------------------------------------------------------------------
+TS_DEV void lm_rows(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t, uint32_t tag) {
+    const uint32_t H = p.H;
+    {
+        float v[2], gv[2];
+        gains<2>(c, p.norm, H, gv);
+        poll<2>(c, p.hand + (size_t)(p.L - 1) * hd.block + hd.xo, H, tag, v);
+        stage<2>(c, v, H, gv);
+    }
+    mark(p, c, t, p.L, 0);
+    bar();
+    const float inv = norm_inv(c, H, p.eps);
+    const uint16_t *xs = c.xs();
+    c.ph++;
+    const Split rows = split(p.V, p.NG, c.g);
+    const uint32_t tiles = (rows.count + 15) / 16;
+    constexpr int KS = 4;  // k-steps per wave (H <= 1024)
+    u32x4 xb[KS];
+#pragma unroll
+    for (int j = 0; j < KS; j++) xb[j] = x_frag(c, xs, c.wave * KS + j, H);
+    float *part = (float *)(c.lds + kLmPartOff) + c.wave * kMaxLm;
+    u32x4 a0[KS], a1[KS], a2[KS], a3[KS];
+    // The packed lm_head tiles of this group (decode_step_pack, role 4).
+    const uint32_t KSt = H / 32, LT = lm_tiles(p.V, p.NG);
+    const char *P = (const char *)p.lm_packed + (size_t)c.g * LT * KSt * 1024;
+    auto load = [&](uint32_t ti, u32x4 (&a)[KS]) {
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const uint32_t ks = c.wave * KS + j;
+            const u32x4 *blk = (const u32x4 *)uniform(P + ((size_t)ti * KSt + ks) * 1024);
+            a[j] = ks < KSt ? __builtin_nontemporal_load(blk + c.lane) : u32x4{0, 0, 0, 0};
+        }
+    };
+    auto use = [&](uint32_t ti, const u32x4 (&a)[KS]) {
+        f32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < KS; j++) acc = mfma16(as_bf16x8(a[j]), as_bf16x8(xb[j]), acc);
+        tile_out(c, acc, part, ti);
+    };
+    if (tiles > 0) load(0, a0);
+    if (tiles > 1) load(1, a1);
+    if (tiles > 2) load(2, a2);
+    for (uint32_t i = 0; i < tiles; i += 4) {
+        if (i + 3 < tiles) load(i + 3, a3);
+        use(i, a0);
+        if (i + 1 >= tiles) break;
+        if (i + 4 < tiles) load(i + 4, a0);
+        use(i + 1, a1);
+        if (i + 2 >= tiles) break;
+        if (i + 5 < tiles) load(i + 5, a1);
+        use(i + 2, a2);
+        if (i + 3 >= tiles) break;
+        if (i + 6 < tiles) load(i + 6, a2);
+        use(i + 3, a3);
+    }
+    mark(p, c, t, p.L, 1);
+    bar();
+    // Row r: the waves' partials in wave order, then the best of this thread's rows.
+    const float *lp = (const float *)(c.lds + kLmPartOff);
+    float bv = -INFINITY;
+    uint32_t bi = p.V;
+    for (uint32_t r = c.tid; r < rows.count; r += kT) {
+        float x = 0.0f;
+#pragma unroll
+        for (uint32_t w = 0; w < kW; w++) x += lp[w * kMaxLm + r];
+        x *= inv;
+        const uint32_t row = rows.first + r;
+        p.logits[row] = x;
+        if (x > -INFINITY) better(bv, bi, x, row);  // NaN and -inf never win
+    }
+#ifdef TS_FINE
+    mark(p, c, t, p.L, 3);
+#endif
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const uint32_t oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+    float *best = (float *)(c.lds + kBestOff);
+    if (c.lane == 0) {
+        best[2 * c.wave] = bv;
+        best[2 * c.wave + 1] = __uint_as_float(bi);
+    }
+    bar();
+    uint64_t *am = p.hand + hd.am;
+    if (c.tid == 0) {
+        float v = -INFINITY;
+        uint32_t i = p.V;
+        for (uint32_t w = 0; w < kW; w++) better(v, i, best[2 * w], __float_as_uint(best[2 * w + 1]));
+        st_tag(am + 2 * c.g, __float_as_uint(v), tag);
+        st_tag(am + 2 * c.g + 1, i, tag);
+    }
+#ifdef TS_FINE
+    mark(p, c, t, p.L, 4);
+#endif
+}
+
+// Every group's best, reduced in group order (ties to the lower index): the token.
+TS_DEV uint32_t pick(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t, uint32_t tag) {
+    uint64_t *am = p.hand + hd.am;
+    float *pk = (float *)(c.lds + kPickOff);
+    for (uint32_t i = c.tid; i < 2 * p.NG; i += kT) pk[i] = poll1(c, am + i, tag);
+#ifdef TS_FINE
+    mark(p, c, t, p.L, 5);
+#endif
+    bar();
+    if (c.wave == 0) {
+        float v = -INFINITY;
+        uint32_t i = p.V;
+        for (uint32_t w = c.lane; w < p.NG; w += 64) {
+            const uint32_t xi = __float_as_uint(pk[2 * w + 1]);
+            if (xi < p.V) better(v, i, pk[2 * w], xi);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(v, o, 64);
+            const uint32_t oi = __shfl_xor(i, o, 64);
+            better(v, i, ov, oi);
+        }
+        if (c.lane == 0) c.ctl[kTok] = i;
+    }
+    bar();
+    mark(p, c, t, p.L, 2);
+    const uint32_t tok = c.ctl[kTok];
+    return tok < p.V ? tok : 0u;  // no finite logit (an aborted launch): any row of the table
+}
+
+// ---------------------------------------------------------------------------
+// Product roles. The group's outputs [s.first, s.first + s.count) of one matrix, as
+// TILES 16-row tiles (gate/up: TILES / 2 gate tiles, then the matching up tiles),
+// held in registers: wave w keeps k-steps [KS w, KS w + KS) of every tile. Per
+// layer: poll the input (the RmsNorm gains loaded first; o and down also poll their
+// residual rows), stage it, one barrier, the MFMAs, the partials to LDS, a barrier,
+// each output summed over the waves by one thread and published by consecutive
+// threads (whole lines per store instruction); then the next layer's tiles are
+// loaded into the same registers.
+// ---------------------------------------------------------------------------
+template <uint32_t KIND, int TILES, int KS, int NX>
+TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t idx, uint32_t count) {
+    const uint32_t H = p.H, F = p.F, QD = p.Hq * 128, QKV = (p.Hq + 2 * p.Hkv) * 128;
+    const uint32_t N = KIND == kQkv ? QKV : (KIND == kGu ? F : H);
+    const uint32_t K = KIND == kQkv || KIND == kGu ? H : (KIND == kO ? QD : F);
+    const Split s = split(N, count, idx);
+    constexpr int OT = KIND == kGu ? TILES / 2 : TILES;  // tiles of outputs
+    u32x4 w[TILES][KS];
+    // The packed tiles (decode_step_pack): tile t, k-step ks of this group is 1 KB at
+    // ((idx * TILES + t) * KSt + ks) KiB, lane l's 16 bytes at l * 16.
+    const uint32_t KSt = K / 32;
+    auto load = [&](uint32_t l) {
+        const char *P = (const char *)p.packed[l][KIND] + (size_t)idx * TILES * KSt * 1024;
+#pragma unroll
+        for (int t = 0; t < TILES; t++) {
+#pragma unroll
+            for (int j = 0; j < KS; j++) {
+                const uint32_t ks = c.wave * KS + j;
+                const u32x4 *blk = (const u32x4 *)uniform(P + ((size_t)t * KSt + ks) * 1024);
+                w[t][j] = ks < KSt ? __builtin_nontemporal_load(blk + c.lane) : u32x4{0, 0, 0, 0};
+            }
+        }
+    };
+    load(0);
+
+    uint32_t tok = p.tok[0];
+    const uint32_t pos0 = p.pos[0];
+    for (uint32_t t = 0; t < p.steps; t++) {
+        const uint32_t tag = p.epoch + t;
+        for (uint32_t l = 0; l < p.L; l++) {
+            const uint64_t *blk = p.hand + (size_t)l * hd.block;
+            const uint64_t *prev = l ? blk - hd.block : nullptr;
+            // Input (the RmsNorm gains loaded first), and for o and down the residual
+            // rows (one word a thread, polled with the input).
+            float v[NX], gv[NX];
+            const uint32_t n = K;
+            gains<NX>(c, KIND == kQkv ? p.ln1[l] : (KIND == kGu ? p.ln2[l] : nullptr), n, gv);
+            const bool has_res = (KIND == kO || KIND == kDn) && c.tid < s.count;
+            const uint64_t *res_src = nullptr;
+            float rv = 0.0f;
+            if (has_res) {
+                if (KIND == kO) {
+                    if (prev) res_src = prev + hd.xo + s.first + c.tid;
+                    else rv = bf16_float(p.embed[(size_t)tok * H + s.first + c.tid]);
+                } else {
+                    res_src = blk + hd.x2 + s.first + c.tid;
+                }
+            }
+            if (KIND == kQkv && !prev) {
+#pragma unroll
+                for (int k = 0; k < NX; k++) {
+                    const uint32_t i = c.tid + kT * k;
+                    v[k] = i < n ? bf16_float(p.embed[(size_t)tok * H + i]) : 0.0f;
+                }
+            } else {
+                const uint64_t *in = KIND == kQkv ? prev + hd.xo
+                                                  : (KIND == kO ? blk + hd.att : (KIND == kGu ? blk + hd.x2 : blk + hd.hf));
+                poll<NX>(c, in, n, tag, v, res_src, &rv);
+            }
+            if (has_res) c.res()[c.tid] = rv;
+            stage<NX>(c, v, n, gv);
+            mark(p, c, t, l, 0);
+            bar();
+            const float inv = KIND == kQkv || KIND == kGu ? norm_inv(c, n, p.eps) : 1.0f;
+            const uint16_t *xs = c.xs();
+            const float *res = c.res();
+            c.ph++;
+            if (s.count) {
+#ifdef TS_FINE
+                mark(p, c, t, l, 2);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                mark(p, c, t, l, 3);
+#endif
+                float *part = c.part();
+                f32x4 acc[TILES];
+#pragma unroll
+                for (int t2 = 0; t2 < TILES; t2++) acc[t2] = f32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < KS; j++) {
+                    const u32x4 xb = x_frag(c, xs, c.wave * KS + j, K);
+#pragma unroll
+                    for (int t2 = 0; t2 < TILES; t2++) acc[t2] = mfma16(as_bf16x8(w[t2][j]), as_bf16x8(xb), acc[t2]);
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < TILES; t2++) tile_out(c, acc[t2], part + c.wave * 64, t2);
+#ifdef TS_FINE
+                mark(p, c, t, l, 4);
+#endif
+                bar();
+                if (c.tid < s.count) {
+                    const uint32_t o = c.tid;
+                    float x = 0.0f;
+#pragma unroll
+                    for (uint32_t w2 = 0; w2 < kW; w2++) x += part[w2 * 64 + o];
+                    float y;
+                    if (KIND == kQkv) {
+                        y = x * inv;
+                    } else if (KIND == kGu) {
+                        float u = 0.0f;
+#pragma unroll
+                        for (uint32_t w2 = 0; w2 < kW; w2++) u += part[w2 * 64 + OT * 16 + o];
+                        const float gt = x * inv, up = u * inv;
+                        y = gt / (1.0f + expf(-gt)) * up;
+                    } else {
+                        y = res[o] + x;
+                    }
+                    uint64_t *out = (uint64_t *)(blk + (KIND == kQkv ? hd.qkv : (KIND == kO ? hd.x2
+                                                                                : (KIND == kGu ? hd.hf : hd.xo))));
+                    st_tag(out + s.first + o, __float_as_uint(y), tag);
+                }
+                mark(p, c, t, l, 1);
+                // The next layer's tiles (the first layer's after the lm_head).
+#ifndef TS_NOPF
+                if (l + 1 < p.L) load(l + 1);
+#endif
+            }
+        }
+        lm_rows(p, c, hd, t, tag);
+        // The first layer's tiles, issued once the lm_head has streamed (its registers
+        // are free then) and after the token's poll (the memory counter retires in
+        // order: a poll issued behind them would wait for them).
+        if (KIND == kQkv || KIND == kO) tok = pick(p, c, hd, t, tag);
+#ifndef TS_NOPF
+        load(0);  // unconditional (also after the last step): the registers are dead across the lm_head
+#endif
+        if (KIND == kQkv && idx == 0 && c.tid == 0) {
+            p.hist[pos0 + t + 1] = tok;
+            if (t + 1 == p.steps) {
+                p.pos[0] = pos0 + p.steps;
+                p.tok[0] = tok;
+            }
+        }
+    }
 }
 
 // RmsNorm over a 128-wide head held as (d, d + 64) in lane d, then the Halves
 // rotation of that pair (engine/ir/interp/src/cpu.rs:36-47, 371-377).
 TS_DEV void norm_rope(float &a, float &b, float ga, float gb, float cs, float sn, float eps) {
-    const float s = wave_sum(a * a + b * b);
+    const float s = wave_total(a * a + b * b);
     const float inv = 1.0f / sqrtf(s / 128.0f + eps);
     a = a * (inv * ga);
     b = b * (inv * gb);
@@ -331,563 +593,304 @@ TS_DEV void norm_rope(float &a, float &b, float ga, float gb, float cs, float sn
     b = rb;
 }
 
-// Optional phase stamps of the first step (thread 0 of every group): slot 2 ph
-// when the phase's input is staged, 2 ph + 1 when its outputs are stored, 8 when
-// the group's attention is done; row L: lm_head input, chunks done, token.
-TS_DEV void mark(const DecodeStepArgs &p, const Ctx &c, uint32_t g, uint32_t t, uint32_t l, uint32_t k) {
-    if (p.marks && t == 0 && c.tid == 0) p.marks[((size_t)g * (p.L + 2) + l) * 10 + k] = now();
-}
-
-constexpr uint32_t kAttBars = 4;  // barriers of attention()
-
-// Sums (maxima) over the four 16-lane rows of a wave, in every lane: lanes j, j + 16,
-// j + 32 and j + 48 end with the same total (gfx950 permlane swaps: VALU, no LDS).
-TS_DEV float rows4_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-TS_DEV float rows4_max(float x) {
-    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-
-// Attention of q head `h` (kv head a = h / 2) at position pos over kept rows
-// [0, pos] (engine/ir/interp/src/cpu.rs:141-167, 293-351): the raw q/k/v rows
-// come from the qkv hand-off; q and the new k are normalized and rotated, the new
-// k and v rows are appended (bf16, by the even head of the pair), and the head's
-// output is published. One group per q head: the two heads of a GQA pair run
-// side by side on two CUs (each loads the pair's kept rows) instead of one
-// after the other on one.
-// Lanes: key = lane / 16 of a 4-key block, dims 8 (lane % 16) .. +8; a wave takes
-// blocks wave + kCW i, kPre of them per softmax pass (one max and one sum per pass,
-// then the running (max, sum, acc) rescaled once per pass).
-TS_DEV void attention(const DecodeStepArgs &p, const Plan &pl, const Hand &hd, Ctx &c, uint32_t l, uint32_t h,
-                      uint32_t pos, uint32_t tag) {
-    const uint32_t lane = c.lane, wave = c.wave, a = h >> 1;
-#define AMARK(k) do { if (l == 5 && tag == p.epoch) mark(p, c, h, 0, p.L + 1, k); } while (0)
-    AMARK(0);
+// ---------------------------------------------------------------------------
+// Attention role: q head h (kv head a = h / (heads / kv heads)) at position pos over
+// kept rows [0, pos] (engine/ir/interp/src/cpu.rs:141-167, 293-351). Lanes: key
+// lane / 16 of a 4-key block, dims 8 (lane % 16) .. +8; wave w takes blocks w + kW i.
+// Scores in base 2 (dot(q, k) * scale * log2 e, v_exp_f32). The raw q/k/v rows come
+// from the qkv hand-off; q and the new k are normalized and rotated, and the new k
+// and v rows appended (bf16) after the head's output is published. Every q head of
+// kv head a appends the same row: the same words through the same arithmetic give
+// the same bits, so the row's value never depends on which write lands last. A
+// group's own append is waited for (vmcnt) before the barrier that ends the layer,
+// and the row is read only at later steps (reads stop at pos - 1 until it exists),
+// through this CU's caches, which never held it before.
+// ---------------------------------------------------------------------------
+TS_DEV void att_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t h) {
+    const uint32_t lane = c.lane, wave = c.wave;
     const uint32_t kr = lane >> 4, part = lane & 15;
-    const uint32_t Hkv = p.Hkv, shift = p.page_shift, mask = (1u << shift) - 1;
-    const uint16_t *kc = p.k_cache[l], *vc = p.v_cache[l];
-    const uint32_t nblk = (pos >> 2) + 1;                                 // 4-key blocks in [0, pos]
-    const uint32_t mine = nblk > wave ? (nblk - wave + kCW - 1) / kCW : 0;  // this wave's blocks
-    float *raw = c.xa + 2560, *qs = c.xa, *pm = c.xa + 384, *pl_ = c.xa + 400, *po = c.xa + 512;
-    uint16_t *kn = (uint16_t *)(c.xa + 256), *vn = (uint16_t *)(c.xa + 320);
-    const uint32_t last = pos ? pos - 1 : 0u;  // kept rows before pos exist; pos arrives in LDS
-
-    // Kept rows of earlier positions: the first kPre blocks of this wave, now.
-    u32x4 kk[kPre], vv[kPre];
-#pragma unroll
-    for (int i = 0; i < kPre; i++) {
-        const uint32_t key = min(4 * (wave + kCW * i) + kr, last);
-        const uint64_t row = ((uint64_t)c.tbl[key >> shift] << shift) | (key & mask);
-        const size_t e = (row * Hkv + a) * 128 + 8 * part;
-        kk[i] = *(const u32x4 *)(kc + e);
-        vv[i] = *(const u32x4 *)(vc + e);
-    }
-    float ga = 0.0f, gb = 0.0f;
-    if (wave == 0) { ga = p.q_norm[l][lane]; gb = p.q_norm[l][lane + 64]; }
-    if (wave == 1) { ga = p.k_norm[l][lane]; gb = p.k_norm[l][lane + 64]; }
-    const float2 cs = ((const float2 *)p.rope)[(size_t)pos * 64 + lane];
-    AMARK(1);
-    // q head h, then k and v of head a: 384 words in 3 runs of 128, one per thread.
-    static_assert(kCT >= 384, "one hand-off word per thread");
-    if (c.tid < 384) {
-        const uint64_t *blk = p.hand + hd.qkv + (size_t)l * hd.block;
-        const uint32_t r = c.tid >> 7, d = c.tid & 127;
-        const uint32_t gi = r == 0 ? h * 128 + d : (r == 1 ? pl.QD + a * 128 + d : pl.QD + (Hkv + a) * 128 + d);
-        uint64_t w = ld_tag(blk + gi);
-        uint64_t t0 = 0;
-        uint32_t it = 0;
-        while ((uint32_t)(w >> 32) != tag && spin(c, it, t0)) w = ld_tag(blk + gi);
-        raw[c.tid] = __uint_as_float((uint32_t)w);
-    }
-    AMARK(2);
-    bar();  // 1
-    AMARK(3);
-    if (wave < 3) {
-        float x0 = raw[wave * 128 + lane], x1 = raw[wave * 128 + lane + 64];
-        if (wave < 2) norm_rope(x0, x1, ga, gb, cs.x, cs.y, p.eps);
-        if (wave == 0) {
-            qs[lane] = x0;
-            qs[lane + 64] = x1;
-        } else {
-            const uint16_t b0 = bf16_bits(x0), b1 = bf16_bits(x1);
-            uint16_t *dst = wave == 1 ? kn : vn;
-            dst[lane] = b0;
-            dst[lane + 64] = b1;
-            // The new row joins the kept rows (Store::append, engine/ir/interp/src/run.rs:122-198),
-            // written once per pair (the odd head computes the same row).
-            if ((h & 1) == 0) {
-                const uint64_t row = ((uint64_t)c.tbl[pos >> shift] << shift) | (pos & mask);
-                uint16_t *cache = (wave == 1 ? p.k_cache[l] : p.v_cache[l]) + (row * Hkv + a) * 128;
-                // Agent scope: the odd head reads this row at the next step from
-                // another CU (perhaps another XCD, whose L2 this store would miss).
-                __hip_atomic_store(cache + lane, b0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(cache + lane + 64, b1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-    }
-    bar();  // 2
-    AMARK(4);
-
-    float q[8];
-    {
-        const float4 t0 = *(const float4 *)&qs[8 * part], t1 = *(const float4 *)&qs[8 * part + 4];
-        q[0] = t0.x; q[1] = t0.y; q[2] = t0.z; q[3] = t0.w;
-        q[4] = t1.x; q[5] = t1.y; q[6] = t1.z; q[7] = t1.w;
-    }
-    const u32x4 knew = *(const u32x4 *)(kn + 8 * part), vnew = *(const u32x4 *)(vn + 8 * part);
-    float m = -INFINITY, ls = 0.0f, o[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = 0.0f;
-
-    for (uint32_t i0 = 0; i0 < mine; i0 += kPre) {
-        if (i0) {  // later passes (contexts past kCW kPre blocks): load this pass now
+    const uint32_t Hkv = p.Hkv, a = h / (p.Hq / Hkv), shift = p.page_shift, mask = (1u << shift) - 1;
+    const uint32_t QD = p.Hq * 128;
+    float *raw = (float *)(c.lds + kAttOff);   // [384]: q h, k a, v a
+    float *qs = raw + 384;                     // [128]
+    uint16_t *kn = (uint16_t *)(qs + 128);     // [128]
+    uint16_t *vn = kn + 128;                   // [128]
+    float *pm = (float *)(vn + 128);           // [kW]
+    float *pl = pm + kW;                       // [kW]
+    float *po = pl + kW;                       // [kW][128]
+    const uint32_t pos0 = p.pos[0];
+    const float sl2 = p.scale * 1.4426950408889634f;
+    for (uint32_t t = 0; t < p.steps; t++) {
+        const uint32_t tag = p.epoch + t, pos = pos0 + t;
+        const uint32_t last = pos ? pos - 1 : 0u;   // kept rows before pos exist
+        const uint32_t nblk = (pos >> 2) + 1;       // 4-key blocks in [0, pos]
+        const uint32_t mine = nblk > wave ? (nblk - wave + kW - 1) / kW : 0;
+        const float2 cs = ((const float2 *)p.rope)[(size_t)pos * 64 + lane];
+        for (uint32_t l = 0; l < p.L; l++) {
+            const uint16_t *kc = p.k_cache[l], *vc = p.v_cache[l];
+            // Kept rows of earlier positions: this wave's first kPre blocks, now.
+            u32x4 kk[kPre], vv[kPre];
 #pragma unroll
             for (int i = 0; i < kPre; i++) {
-                const uint32_t key = min(4 * (wave + kCW * (i0 + i)) + kr, last);
+                const uint32_t key = min(4 * (wave + kW * i) + kr, last);
                 const uint64_t row = ((uint64_t)c.tbl[key >> shift] << shift) | (key & mask);
                 const size_t e = (row * Hkv + a) * 128 + 8 * part;
                 kk[i] = *(const u32x4 *)(kc + e);
                 vv[i] = *(const u32x4 *)(vc + e);
             }
-        }
-        float sc[kPre];
-        bool ok[kPre];
-#pragma unroll
-        for (int i = 0; i < kPre; i++) {
-            const uint32_t key = 4 * (wave + kCW * (i0 + i)) + kr;
-            ok[i] = key <= pos;  // past the wave's blocks too: key >= 4 nblk > pos
-            const u32x4 kv = key == pos ? knew : kk[i];
-            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-            float s0 = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                s0 += q[2 * e] * lo_bf16(kw[e]);
-                s0 += q[2 * e + 1] * hi_bf16(kw[e]);
+            float ga = 0.0f, gb = 0.0f;
+            if (wave == 0) { ga = p.q_norm[l][lane]; gb = p.q_norm[l][lane + 64]; }
+            if (wave == 1) { ga = p.k_norm[l][lane]; gb = p.k_norm[l][lane + 64]; }
+            // q head h, then k and v of head a: one word a thread.
+            if (c.tid < 384) {
+                const uint64_t *blk = p.hand + hd.qkv + (size_t)l * hd.block;
+                const uint32_t r = c.tid >> 7, d = c.tid & 127;
+                const uint32_t gi = r == 0 ? h * 128 + d : QD + ((r - 1) * Hkv + a) * 128 + d;
+                raw[c.tid] = poll1(c, blk + gi, tag);
             }
-            sc[i] = ok[i] ? row16_sum(s0) * p.scale : -INFINITY;
-        }
-        float bm = sc[0];
-#pragma unroll
-        for (int i = 1; i < kPre; i++) bm = fmaxf(bm, sc[i]);
-        const float mn = fmaxf(m, rows4_max(bm));  // finite: key 4 wave <= pos
-        const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
-        float acc[8], sum = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; e++) acc[e] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kPre; i++) {
-            const float pk = ok[i] ? expf(sc[i] - mn) : 0.0f;
-            sum += pk;
-            const u32x4 vx = (4 * (wave + kCW * (i0 + i)) + kr) == pos ? vnew : vv[i];
-            const uint32_t vw[4] = {ok[i] ? vx.x : 0u, ok[i] ? vx.y : 0u, ok[i] ? vx.z : 0u, ok[i] ? vx.w : 0u};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                acc[2 * e] += pk * lo_bf16(vw[e]);
-                acc[2 * e + 1] += pk * hi_bf16(vw[e]);
-            }
-        }
-        ls = ls * alpha + rows4_sum(sum);
-        m = mn;
-#pragma unroll
-        for (int e = 0; e < 8; e++) o[e] = o[e] * alpha + acc[e];
-    }
-    AMARK(5);
-    // Sum the four key rows; lanes of row 0 hold the wave's 128 partial sums.
-#pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = rows4_sum(o[e]);
-    if (kr == 0) {
-        *(float4 *)&po[wave * 128 + 8 * part] = make_float4(o[0], o[1], o[2], o[3]);
-        *(float4 *)&po[wave * 128 + 8 * part + 4] = make_float4(o[4], o[5], o[6], o[7]);
-    }
-    if (lane == 0) {
-        pm[wave] = m;
-        pl_[wave] = ls;
-    }
-    bar();  // 3
-    AMARK(6);
-    if (c.tid < 128) {
-        const uint32_t d = c.tid;
-        float M = -INFINITY;
-        for (uint32_t w = 0; w < kCW; w++) M = fmaxf(M, pm[w]);
-        float L = 0.0f, O = 0.0f;
-        for (uint32_t w = 0; w < kCW; w++) {
-            const float f = pm[w] == -INFINITY ? 0.0f : expf(pm[w] - M);
-            L += pl_[w] * f;
-            O += po[w * 128 + d] * f;
-        }
-        st_tag(p.hand + hd.att + (size_t)l * hd.block + h * 128 + d, __float_as_uint(O / L), tag);
-    }
-    AMARK(7);
-    bar();  // 4: the next phase stages its input over this scratch
-    AMARK(8);
-}
-
-TS_DEV void better(float &bv, uint32_t &bi, float v, uint32_t i) {
-    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
-}
-TS_DEV void wave_best(float &bv, uint32_t &bi) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float v = __shfl_xor(bv, o, 64);
-        const uint32_t i = __shfl_xor(bi, o, 64);
-        better(bv, bi, v, i);
-    }
-}
-
-// One product phase of a layer.
-struct Phase {
-    const uint64_t *in;  // tagged input; null: the embedding row of the step's token
-    const float *gain;   // RmsNorm gain; null: none
-    uint64_t *out;       // tagged outputs, from row `first`
-    uint32_t n, ua, Ra, ub, R, K, first;
-    uint32_t kind;       // 0: value * inv; 1: xr[first + r] + value; 2: silu(gate) * up
-    bool keep_raw;
-};
-
-// Stage the input, barrier (the DMA waves have landed the rows), products,
-// barrier, publish.
-template <int NX>
-TS_DEV void run_phase(const DecodeStepArgs &p, Ctx &c, const Phase &f, uint32_t tag, uint32_t tok, uint32_t g,
-                      uint32_t t, uint32_t l, uint32_t ph) {
-    float v[NX], gv[NX];
-#pragma unroll
-    for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kCT * k;
-        gv[k] = f.gain && i < f.n ? f.gain[i] : 1.0f;
-    }
-    if (f.in) {
-        poll(c, f.in, f.n, tag, v);
-    } else {
-#pragma unroll
-        for (int k = 0; k < NX; k++) {
-            const uint32_t i = c.tid + kCT * k;
-            v[k] = i < f.n ? bf16_float(p.embed[(size_t)tok * f.n + i]) : 0.0f;
-        }
-    }
-    stage(c, v, f.n, gv, f.keep_raw);
-    mark(p, c, g, t, l, 2 * ph);
-    bar();
-    const float inv = f.gain ? norm_inv(c, f.n, p.eps) : 1.0f;
-    const uint32_t S = gemv_part(c, f.ua, f.Ra, f.ub, f.R, f.K, c.red);
-    bar();
-    const uint32_t outs = f.kind == 2 ? f.Ra : f.R;
-    if (c.tid < outs) {
-        const float x = row_value(c.red, c.tid, S);
-        float y;
-        if (f.kind == 0) {
-            y = x * inv;
-        } else if (f.kind == 1) {
-            y = c.xr[f.first + c.tid] + x;
-        } else {
-            const float gt = x * inv, up = row_value(c.red, f.Ra + c.tid, S) * inv;
-            y = gt / (1.0f + expf(-gt)) * up;
-        }
-        st_tag(f.out + f.first + c.tid, __float_as_uint(y), tag);
-    }
-    mark(p, c, g, t, l, 2 * ph + 1);
-}
-
-// The compute waves of group g. Barrier schedule per step (mirrored by dma()):
-// per layer 2 per phase x 4 phases (+ kAttBars after phase 0 in groups below
-// kv_heads); then 1 for the lm_head input, 1 per chunk, 2 for the token.
-TS_DEV void compute(const DecodeStepArgs &p, Ctx &c, uint32_t g) {
-    const Plan pl = plan(p, g);
-    const Hand hd = hand(p, pl);
-    const uint32_t H = p.H, F = p.F;
-    const uint32_t pos0 = p.pos[0];
-    uint32_t tok = p.tok[0];
-    uint32_t U = 0;  // stream cursor (units)
-    for (uint32_t t = 0; t < p.steps; t++) {
-        const uint32_t tag = p.epoch + t, pos = pos0 + t;
-        for (uint32_t l = 0; l < p.L; l++) {
-            uint64_t *blk = p.hand + (size_t)l * hd.block;
-            const uint32_t Uq = U, Uo = Uq + pl.uq, Ug = Uo + pl.uo, Uu = Ug + pl.ug, Ud = Uu + pl.ug;
-            U = Ud + pl.ud;
-            for (uint32_t ph = 0; ph < 4; ph++) {
-                Phase f;
-                if (ph == 0) {  // RmsNorm(ln1), qkv rows
-                    f = {l ? blk - hd.block + hd.xo : nullptr, p.ln1[l], blk + hd.qkv, H, Uq, pl.q.count, Uq,
-                         pl.q.count, H, pl.q.first, 0u, true};
-                } else if (ph == 1) {  // o rows + residual
-                    f = {blk + hd.att, nullptr, blk + hd.x2, pl.QD, Uo, pl.o.count, Uo, pl.o.count, pl.QD,
-                         pl.o.first, 1u, false};
-                } else if (ph == 2) {  // RmsNorm(ln2), gate and up rows, silu(gate) * up
-                    f = {blk + hd.x2, p.ln2[l], blk + hd.hf, H, Ug, pl.f.count, Uu, 2 * pl.f.count, H, pl.f.first,
-                         2u, true};
-                } else {  // down rows + residual
-                    f = {blk + hd.hf, nullptr, blk + hd.xo, F, Ud, pl.o.count, Ud, pl.o.count, F, pl.o.first, 1u,
-                         false};
-                }
-                if (ph & 1)
-                    run_phase<kNX>(p, c, f, tag, tok, g, t, l, ph);
-                else
-                    run_phase<kNH>(p, c, f, tag, tok, g, t, l, ph);
-                if (ph == 0 && g < p.Hq) {
-                    attention(p, pl, hd, c, l, g, pos, tag);
-                    mark(p, c, g, t, l, 8);
+            mark(p, c, t, l, 0);
+            bar();
+            if (wave < 3) {
+                float x0 = raw[wave * 128 + lane], x1 = raw[wave * 128 + lane + 64];
+                if (wave < 2) norm_rope(x0, x1, ga, gb, cs.x, cs.y, p.eps);
+                if (wave == 0) {
+                    qs[lane] = x0;
+                    qs[lane + 64] = x1;
+                } else {
+                    uint16_t *dst = wave == 1 ? kn : vn;
+                    dst[lane] = bf16_bits(x0);
+                    dst[lane + 64] = bf16_bits(x1);
                 }
             }
-        }
-        // --- final RmsNorm, lm_head rows, greedy pick ---
-        {
-            float v[kNH], gn[kNH];
+            bar();
+            float q[8];
+            {
+                const float4 q0 = *(const float4 *)&qs[8 * part], q1 = *(const float4 *)&qs[8 * part + 4];
+                q[0] = q0.x; q[1] = q0.y; q[2] = q0.z; q[3] = q0.w;
+                q[4] = q1.x; q[5] = q1.y; q[6] = q1.z; q[7] = q1.w;
+            }
+            const u32x4 knew = *(const u32x4 *)(kn + 8 * part), vnew = *(const u32x4 *)(vn + 8 * part);
+            float m = -INFINITY, ls = 0.0f, o[8];
 #pragma unroll
-            for (int k = 0; k < kNH; k++) {
-                const uint32_t i = c.tid + kCT * k;
-                gn[k] = i < H ? p.norm[i] : 1.0f;
-            }
-            poll(c, p.hand + (size_t)(p.L - 1) * hd.block + hd.xo, H, tag, v);
-            stage(c, v, H, gn, false);
-        }
-        mark(p, c, g, t, p.L, 0);
-        bar();  // lm input staged; chunk 0 landed
-        const float inv = norm_inv(c, H, p.eps);
-        float bv = -INFINITY;
-        uint32_t bi = p.V;
-        for (uint32_t ch = 0; ch < pl.chunks; ch++) {
-            const uint32_t r0 = ch * kChunk, rows = min(kChunk, pl.v.count - r0);
-            const uint32_t Uc = U;
-            U += units(rows * H * 2);
-            // Chunks alternate halves of the partials: wave 0 reads chunk ch's after
-            // the barrier while the other waves write chunk ch + 1's.
-            float *red = c.red + (ch & 1) * 64;
-            const uint32_t S = gemv_part(c, Uc, rows, Uc, rows, H, red);
-            bar();  // chunk ch consumed; chunk ch + 1 landed
-            if (c.wave == 0) {
-                float v = -INFINITY;
-                uint32_t i = p.V;
-                if (c.lane < rows) {
-                    const uint32_t row = pl.v.first + r0 + c.lane;
-                    const float x = row_value(red, c.lane, S) * inv;
-                    p.logits[row] = x;
-                    if (x > -INFINITY) { v = x; i = row; }  // NaN and -inf never win
-                }
-                wave_best(v, i);
-                better(bv, bi, v, i);
-            }
-        }
-        mark(p, c, g, t, p.L, 1);
-        uint64_t *am = p.hand + hd.am;
-        if (c.tid == 0) {
-            st_tag(am + 2 * g, __float_as_uint(bv), tag);
-            st_tag(am + 2 * g + 1, bi, tag);
-        }
-        {
-            float v[kNA];
-            poll(c, am, 2 * p.NG, tag, v);
+            for (int e = 0; e < 8; e++) o[e] = 0.0f;
+
+            for (uint32_t i0 = 0; i0 < mine; i0 += kPre) {
+                if (i0) {  // contexts past kW kPre blocks: load this pass now
 #pragma unroll
-            for (int k = 0; k < kNA; k++)
-                if (c.tid + kCT * k < 2 * p.NG) c.red[128 + c.tid + kCT * k] = v[k];
-        }
-        bar();
-        if (c.wave == 0) {
-            float v = -INFINITY;
-            uint32_t i = p.V;
-            for (uint32_t w = c.lane; w < p.NG; w += 64) {
-                const float x = c.red[128 + 2 * w];
-                const uint32_t xi = __float_as_uint(c.red[128 + 2 * w + 1]);
-                if (xi < p.V) better(v, i, x, xi);
-            }
-            wave_best(v, i);
-            if (c.lane == 0) c.ctl[kTok] = i;
-        }
-        bar();
-        mark(p, c, g, t, p.L, 2);
-        tok = c.ctl[kTok];
-        if (tok >= p.V) tok = 0;  // no finite logit (an aborted launch): any row of the table
-        if (g == 0 && c.tid == 0) p.hist[pos + 1] = tok;
-    }
-    if (g == 0 && c.tid == 0) {
-        p.pos[0] = pos0 + p.steps;
-        p.tok[0] = tok;
-    }
-}
-
-// Wait until at most n of this wave's DMA loads are in flight (n rounded down to a
-// multiple of 8: the vmcnt field is an immediate).
-TS_DEV void wait_vm(uint32_t n) {
-    switch (n >> 3) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 1: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
-    case 5: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(48)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(56)" ::: "memory"); break;
-    }
-}
-
-// A DMA wave: streams the units u with u % 2 == dw of the group's weight stream
-// (per step and layer the qkv, o, gate, up and down rows, then the lm_head rows
-// in chunks) into ring slot u % kRing, and walks the compute's barrier schedule.
-struct Dma {
-    const DecodeStepArgs *p;
-    Plan pl;
-    uint32_t dw, lane, ring;
-    uint32_t total;      // units of the whole launch
-    uint32_t U;          // next unit to issue
-    uint32_t freed;      // units whose slots may be reused: unit u needs u < freed + kRing
-    uint32_t mine;       // this wave's units issued so far
-    uint32_t inflight;   // of those, possibly still in flight
-    uint32_t burst;      // loads per wave issued ahead of need per barrier
-    // the segment under the cursor
-    uint32_t seg, seg_u, seg_n, seg_bytes;
-    const char *seg_base;
-
-    TS_DEV void open_segment() {
-        const DecodeStepArgs &a = *p;
-        const uint32_t per = 5 * a.L + pl.chunks, js = __builtin_amdgcn_readfirstlane(seg % per), H = a.H, F = a.F;
-        if (js < 5 * a.L) {
-            const uint32_t l = js / 5, s = js % 5;
-            if (s == 0) {
-                seg_base = (const char *)(a.qkv[l] + (size_t)pl.q.first * H); seg_bytes = pl.q.count * H * 2;
-            } else if (s == 1) {
-                seg_base = (const char *)(a.o[l] + (size_t)pl.o.first * pl.QD); seg_bytes = pl.o.count * pl.QD * 2;
-            } else if (s == 4) {
-                seg_base = (const char *)(a.down[l] + (size_t)pl.o.first * F); seg_bytes = pl.o.count * F * 2;
-            } else {
-                seg_base = (const char *)(a.gate_up[l] + (size_t)((s == 3 ? F : 0) + pl.f.first) * H);
-                seg_bytes = pl.f.count * H * 2;
-            }
-        } else {
-            const uint32_t r0 = (js - 5 * a.L) * kChunk;
-            seg_base = (const char *)(a.embed + (size_t)(pl.v.first + r0) * H);
-            seg_bytes = min(kChunk, pl.v.count - r0) * H * 2;
-        }
-        seg_n = units(seg_bytes);
-        seg_u = 0;
-    }
-
-    // Issue the next units the ring has room for: at least those below `need`, else
-    // at most kBurst of this wave's per barrier (a long burst would hold the barrier
-    // up; the compute meets a dozen barriers per layer).
-    TS_DEV void issue(uint32_t need) {
-        const uint32_t limit = min(total, min(freed + kRing, max(U + 2 * burst, need)));
-        while (U < limit) {
-            if (seg_u >= seg_n) {
-                seg++;
-                open_segment();
-                continue;
-            }
-            const uint32_t n = min(seg_n - seg_u, limit - U);
-            // this wave's units of the run: U + k with (U + k) % 2 == dw
-            for (uint32_t k = (U & 1) == dw ? 0u : 1u; k < n; k += 2) {
-                if (inflight >= kMaxOut) {
-                    wait_vm(kMaxOut - 8);
-                    inflight = kMaxOut - 8;
+                    for (int i = 0; i < kPre; i++) {
+                        const uint32_t key = min(4 * (wave + kW * (i0 + i)) + kr, last);
+                        const uint64_t row = ((uint64_t)c.tbl[key >> shift] << shift) | (key & mask);
+                        const size_t e = (row * Hkv + a) * 128 + 8 * part;
+                        kk[i] = *(const u32x4 *)(kc + e);
+                        vv[i] = *(const u32x4 *)(vc + e);
+                    }
                 }
-                const uint32_t off = min((seg_u + k) * 1024 + lane * 16, seg_bytes - 16);
-                __builtin_amdgcn_global_load_lds((const void *)(seg_base + off),
-                                                 (lds_void *)(uintptr_t)(ring + (((U + k) & (kRing - 1)) << 10)), 16,
-                                                 0, 0);
-                mine++;
-                inflight++;
+                float sc[kPre];
+                bool ok[kPre];
+#pragma unroll
+                for (int i = 0; i < kPre; i++) {
+                    const uint32_t key = 4 * (wave + kW * (i0 + i)) + kr;
+                    ok[i] = key <= pos;
+                    const u32x4 kv = key == pos ? knew : kk[i];
+                    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+                    float s0 = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        s0 += q[2 * e] * lo_bf16(kw[e]);
+                        s0 += q[2 * e + 1] * hi_bf16(kw[e]);
+                    }
+                    sc[i] = ok[i] ? row16_sum(s0) * sl2 : -INFINITY;
+                }
+                float bm = sc[0];
+#pragma unroll
+                for (int i = 1; i < kPre; i++) bm = fmaxf(bm, sc[i]);
+                const float mn = fmaxf(m, rows4_max(bm));  // finite: key 4 wave <= pos
+                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+                float acc[8], sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kPre; i++) {
+                    const float pk = ok[i] ? __builtin_amdgcn_exp2f(sc[i] - mn) : 0.0f;
+                    sum += pk;
+                    const u32x4 vx = (4 * (wave + kW * (i0 + i)) + kr) == pos ? vnew : vv[i];
+                    const uint32_t vw[4] = {ok[i] ? vx.x : 0u, ok[i] ? vx.y : 0u, ok[i] ? vx.z : 0u,
+                                            ok[i] ? vx.w : 0u};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        acc[2 * e] += pk * lo_bf16(vw[e]);
+                        acc[2 * e + 1] += pk * hi_bf16(vw[e]);
+                    }
+                }
+                ls = ls * alpha + rows4_sum(sum);
+                m = mn;
+#pragma unroll
+                for (int e = 0; e < 8; e++) o[e] = o[e] * alpha + acc[e];
             }
-            seg_u += n;
-            U += n;
-        }
-    }
-
-    // The barrier after which the compute reads units [0, need) and before which it
-    // has released units [0, free).
-    TS_DEV void barrier(uint32_t need, uint32_t free) {
-        issue(need);  // every unit below `need` is issued (the ring holds a phase)
-        const uint32_t below = dw == 0 ? (need + 1) >> 1 : need >> 1;  // this wave's units < need
-        const uint32_t after = mine - min(mine, below);
-        if (after < inflight) {
-            wait_vm(after);
-            inflight = after & ~7u;
-        }
-        bar();
-        if (free > freed) freed = free;
-    }
-};
-
-TS_DEV void dma(const DecodeStepArgs &p, uint32_t g, uint32_t dw, uint32_t lane, uint32_t ring) {
-    Dma d;
-    d.p = &p;
-    d.pl = plan(p, g);
-    d.dw = dw;
-    d.lane = lane;
-    d.ring = ring;
-    d.total = d.pl.step * p.steps;
-    d.U = 0;
-    d.freed = 0;
-    d.mine = 0;
-    d.inflight = 0;
-    d.burst = kBurst;
-    d.seg = 0;
-    d.open_segment();
-    const Plan &pl = d.pl;
-    uint32_t U = 0;  // the compute's cursor
-    for (uint32_t t = 0; t < p.steps; t++) {
-        for (uint32_t l = 0; l < p.L; l++) {
-            const uint32_t ends[4] = {U + pl.uq, U + pl.uq + pl.uo, U + pl.uq + pl.uo + 2 * pl.ug, U + pl.layer};
-            for (uint32_t ph = 0; ph < 4; ph++) {
-                d.barrier(ends[ph], 0);  // staged input; the phase's rows landed
-                d.barrier(0, ends[ph]);  // products done; its rows released
-                if (ph == 0 && g < p.Hq)
-                    for (uint32_t b = 0; b < kAttBars; b++) d.barrier(0, 0);
+            // Sum the four key rows; lanes of row 0 hold the wave's partial sums.
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = rows4_sum(o[e]);
+            if (kr == 0) {
+                float *dst = po + wave * 128 + 8 * part;
+                *(float4 *)dst = make_float4(o[0], o[1], o[2], o[3]);
+                *(float4 *)(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
             }
-            U += pl.layer;
+            if (lane == 0) {
+                pm[wave] = m;
+                pl[wave] = ls;
+            }
+            bar();
+            if (c.tid < 128) {
+                const uint32_t d = c.tid;
+                float M = -INFINITY;
+                for (uint32_t w = 0; w < kW; w++) M = fmaxf(M, pm[w]);
+                float L = 0.0f, O = 0.0f;
+                for (uint32_t w = 0; w < kW; w++) {
+                    const float f = pm[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(pm[w] - M);
+                    L += pl[w] * f;
+                    O += po[w * 128 + d] * f;
+                }
+                st_tag(p.hand + hd.att + (size_t)l * hd.block + h * 128 + d, __float_as_uint(O / L), tag);
+            }
+            mark(p, c, t, l, 1);
+            // Then the new row joins the kept rows (Store::append,
+            // engine/ir/interp/src/run.rs:122-198), off the chain.
+            if (wave == 1 || wave == 2) {
+                const uint16_t *src = wave == 1 ? kn : vn;
+                const uint64_t row = ((uint64_t)c.tbl[pos >> shift] << shift) | (pos & mask);
+                uint16_t *cache = (wave == 1 ? p.k_cache[l] : p.v_cache[l]) + (row * Hkv + a) * 128;
+                ((uint32_t *)cache)[lane] = ((const uint32_t *)src)[lane];
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            bar();  // the scratch is reused by the next layer
         }
-        d.barrier(pl.chunks ? U + chunk_units(p, pl, 0) : 0, 0);  // lm input; chunk 0 landed
-        // The lm_head chunks: little compute per barrier, so the DMA waves keep the
-        // ring as full as their loads in flight allow.
-        d.burst = kLmBurst;
-        for (uint32_t ch = 0; ch < pl.chunks; ch++) {
-            const uint32_t next = U + chunk_units(p, pl, ch);
-            const uint32_t need = ch + 1 < pl.chunks ? next + chunk_units(p, pl, ch + 1) : 0;
-            d.barrier(need, next);
-            U = next;
-        }
-        d.burst = kBurst;
-        d.barrier(0, 0);
-        d.barrier(0, 0);
+        lm_rows(p, c, hd, t, tag);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
-__global__ __launch_bounds__(kThreads) void decode_step_kernel(DecodeStepArgs p) {
+// Groups without a role: the lm_head only.
+TS_DEV void idle_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd) {
+    for (uint32_t t = 0; t < p.steps; t++) lm_rows(p, c, hd, t, p.epoch + t);
+}
+
+__global__ __launch_bounds__(kT) void decode_step_kernel(DecodeStepArgs p) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    // The wave index is uniform: readfirstlane lets the compiler keep what derives
-    // from it (the DMA cursors, the segment pointers) in scalar registers; as
-    // vector values, the per-layer pointer loads of the DMA waves became vector
-    // loads followed by a wait for every load in flight.
-    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63,
-                   g = blockIdx.x;
-    volatile uint32_t *ctl = (volatile uint32_t *)(lds + kCtlOff);
-    uint32_t *tbl = (uint32_t *)(lds + kTblOff);
-    if (tid < 16) ctl[tid] = 0u;
-    if (g < p.Hq)
-        for (uint32_t i = tid; i < p.kept_pages; i += kThreads) tbl[i] = p.table[i];
-    __syncthreads();
-    if (wave >= kCW) {
-        const uint32_t base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
-        dma(p, g, wave - kCW, lane, base + kRingOff);
-        return;
-    }
+    const uint32_t tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const uint32_t g = blockIdx.x;
     Ctx c;
     c.lds = lds;
-    c.xa = (float *)(lds + kXaOff);
-    c.xr = (float *)(lds + kXrOff);
-    c.red = (float *)(lds + kRedOff);
-    c.ssq = (float *)(lds + kSsqOff);
-    c.tbl = tbl;
-    c.ctl = ctl;
+    c.ctl = (volatile uint32_t *)(lds + kCtlOff);
     c.err = p.error;
+    c.tbl = (uint32_t *)(lds + kTblOff);
     c.tid = tid;
     c.wave = wave;
     c.lane = lane;
-    compute(p, c, g);
+    c.g = g;
+    c.ph = 0;
+    if (tid < 16) c.ctl[tid] = 0u;
+    uint32_t role = kAtt + 1, idx = 0;
+#pragma unroll
+    for (uint32_t r = 0; r <= kAtt; r++)
+        if (g >= p.role_first[r] && g < p.role_first[r] + p.role_count[r]) { role = r; idx = g - p.role_first[r]; }
+    if (role == kAtt)
+        for (uint32_t i = tid; i < p.kept_pages; i += kT) c.tbl[i] = p.table[i];
+    __syncthreads();
+    const Hand hd = hand(p);
+    switch (role) {
+    case kQkv: product_role<kQkv, kTilesQkv, kMaxH / 256, kMaxH / kT>(p, c, hd, idx, p.role_count[kQkv]); break;
+    case kO: product_role<kO, kTilesO, kMaxQD / 256, kMaxQD / kT>(p, c, hd, idx, p.role_count[kO]); break;
+    case kGu: product_role<kGu, kTilesGu, kMaxH / 256, kMaxH / kT>(p, c, hd, idx, p.role_count[kGu]); break;
+    case kDn: product_role<kDn, kTilesDn, kMaxF / 256, kMaxF / kT>(p, c, hd, idx, p.role_count[kDn]); break;
+    case kAtt: att_role(p, c, hd, idx); break;
+    default: idle_role(p, c, hd); break;
+    }
+}
+
+// Outputs a group of each product role can hold.
+constexpr uint32_t kCap[4] = {16 * kTilesQkv, 16 * kTilesO, 16 * kTilesGu / 2, 16 * kTilesDn};
+
+// Groups per role: the fewest that hold every output (attention: one per q head),
+// then spare groups to the role whose groups carry the most weight bytes, in the
+// fewest that lower that load.
+bool plan_roles(uint32_t H, uint32_t Hq, uint32_t Hkv, uint32_t F, uint32_t NG, uint32_t *first, uint32_t *count) {
+    const uint32_t QKV = (Hq + 2 * Hkv) * 128, QD = Hq * 128;
+    const uint64_t n[4] = {QKV, H, F, H};
+    const uint64_t bytes[4] = {2ull * H, 2ull * QD, 4ull * H, 2ull * F};  // per output
+    uint32_t c[4];
+    uint32_t used = Hq;
+    for (int r = 0; r < 4; r++) {
+        c[r] = (uint32_t)((n[r] + kCap[r] - 1) / kCap[r]);
+        used += c[r];
+    }
+    if (used > NG) return false;
+    auto load = [&](int r, uint32_t k) { return ((n[r] + k - 1) / k) * bytes[r]; };
+    uint32_t spare = NG - used;
+    bool done[4] = {false, false, false, false};
+    for (;;) {
+        int best = -1;
+        for (int r = 0; r < 4; r++)
+            if (!done[r] && (best < 0 || load(r, c[r]) > load(best, c[best]))) best = r;
+        if (best < 0) break;
+        uint32_t k = c[best] + 1;
+        while (k <= c[best] + spare && load(best, k) >= load(best, c[best])) k++;
+        if (k > c[best] + spare) {
+            done[best] = true;
+            continue;
+        }
+        spare -= k - c[best];
+        c[best] = k;
+    }
+    uint32_t at = 0;
+    for (int r = 0; r < 4; r++) {
+        first[r] = at;
+        count[r] = c[r];
+        at += c[r];
+    }
+    first[kAtt] = at;
+    count[kAtt] = Hq;
+    return true;
+}
+
+
+// Packed copy of one role's matrix (decode_step_pack): thread i writes the 16 bytes of
+// lane i % 64 of block i / 64 = (group, tile, k-step).
+__global__ __launch_bounds__(256) void pack_kernel(const uint16_t *W, uint16_t *dst, uint32_t N, uint32_t K,
+                                                   uint32_t groups, uint32_t tiles, uint32_t up_off, uint32_t gu,
+                                                   uint64_t chunks) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= chunks) return;
+    const uint32_t KSt = K / 32, lane = (uint32_t)(i & 63);
+    const uint64_t blk = i >> 6;
+    const uint32_t ks = (uint32_t)(blk % KSt), t = (uint32_t)((blk / KSt) % tiles), g = (uint32_t)(blk / KSt / tiles);
+    const Split s = split(N, groups, g);
+    const uint32_t ot = gu ? tiles / 2 : tiles;
+    const uint32_t o = (t % ot) * 16 + (lane & 15);
+    u32x4 v = {0, 0, 0, 0};
+    if (o < s.count) {
+        const uint32_t row = s.first + o + (gu && t >= ot ? up_off : 0u);
+        v = *(const u32x4 *)(W + (size_t)row * K + ks * 32 + (lane >> 4) * 8);
+    }
+    *((u32x4 *)dst + i) = v;
+}
+
+struct PackShape {
+    uint32_t N, K, groups, tiles, up_off, gu;
+};
+
+bool pack_shape(uint32_t H, uint32_t Hq, uint32_t Hkv, uint32_t F, uint32_t V, uint32_t NG, uint32_t role,
+                PackShape *ps) {
+    uint32_t first[5], count[5];
+    if (!plan_roles(H, Hq, Hkv, F, NG, first, count)) return false;
+    const uint32_t QKV = (Hq + 2 * Hkv) * 128, QD = Hq * 128;
+    switch (role) {
+    case kQkv: *ps = {QKV, H, count[kQkv], kTilesQkv, 0, 0}; break;
+    case kO: *ps = {H, QD, count[kO], kTilesO, 0, 0}; break;
+    case kGu: *ps = {F, H, count[kGu], kTilesGu, F, 1}; break;
+    case kDn: *ps = {H, F, count[kDn], kTilesDn, 0, 0}; break;
+    case 4: *ps = {V, H, NG, lm_tiles(V, NG), 0, 0}; break;
+    default: return false;
+    }
+    return true;
 }
 
 }  // namespace
@@ -897,24 +900,36 @@ size_t decode_step_hand_words(uint32_t H, uint32_t L, uint32_t Hq, uint32_t Hkv,
     return L * block + 2 * (size_t)NG;
 }
 
-int decode_step_supported(uint32_t H, uint32_t L, uint32_t Hq, uint32_t Hkv, uint32_t D, uint32_t F,
+int decode_step_supported(uint32_t H, uint32_t L, uint32_t Hq, uint32_t Hkv, uint32_t D, uint32_t F, uint32_t V,
                           uint32_t kept_pages) {
     uint32_t ng = 0;
     int rc = decode_step_groups(&ng);
     if (rc != TS_OK) return rc;
-    if (D != 128 || Hkv == 0 || Hq != 2 * Hkv || Hq > ng || ng > kMaxGroups) return 1;
-    if (L > kStepMaxLayers || H > kMaxH || H % 8 || F % 8 || F > kMaxXa || Hq * 128 > kMaxXa) return 1;
+    if ((V + ng - 1) / ng > kMaxLm) return 1;
+    if (D != 128 || Hkv == 0 || Hq % Hkv || ng > kStepMaxGroups) return 1;
+    if (H % 32 || F % 32) return 1;  // whole 32-deep k-steps
+    if (L > kStepMaxLayers || H > kMaxH || H % 8 || F % 8 || F > kMaxF || Hq * 128 > kMaxQD) return 1;
     if (kept_pages > kMaxPages) return 1;
-    // No group may own more than kRW kCW rows of a phase, and every phase's rows
-    // must fit half the ring.
-    const uint32_t QKV = (Hq + 2 * Hkv) * 128;
-    const uint32_t rq = (QKV + ng - 1) / ng, ro = (H + ng - 1) / ng, rf = (F + ng - 1) / ng;
-    if (rq > kRW * kCW || ro > kRW * kCW || 2 * rf > kRW * kCW) return 1;
-    auto u = [](uint64_t b) { return (b + 1023) / 1024; };
-    if (u((uint64_t)rq * H * 2) > kRing / 2 || u((uint64_t)ro * Hq * 256) > kRing / 2 ||
-        2 * u((uint64_t)rf * H * 2) > kRing / 2 || u((uint64_t)ro * F * 2) > kRing / 2 ||
-        u((uint64_t)kChunk * H * 2) > kRing / 2)
-        return 1;
+    uint32_t first[5], count[5];
+    return plan_roles(H, Hq, Hkv, F, ng, first, count) ? TS_OK : 1;
+}
+
+size_t decode_step_packed_elems(uint32_t H, uint32_t Hq, uint32_t Hkv, uint32_t F, uint32_t V, uint32_t NG,
+                                uint32_t role) {
+    PackShape ps;
+    if (!pack_shape(H, Hq, Hkv, F, V, NG, role, &ps)) return 0;
+    return (size_t)ps.groups * ps.tiles * (ps.K / 32) * 512;
+}
+
+int decode_step_pack(const uint16_t *W, uint16_t *dst, uint32_t H, uint32_t Hq, uint32_t Hkv, uint32_t F, uint32_t V,
+                     uint32_t NG, uint32_t role, void *stream) {
+    PackShape ps;
+    if (!pack_shape(H, Hq, Hkv, F, V, NG, role, &ps) || ps.K % 32)
+        return fail(TS_ERR_ARG, "decode_step_pack: role %u does not fit %u groups", role, NG);
+    const uint64_t chunks = (uint64_t)ps.groups * ps.tiles * (ps.K / 32) * 64;
+    hipLaunchKernelGGL(pack_kernel, dim3((uint32_t)((chunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream, W, dst,
+                       ps.N, ps.K, ps.groups, ps.tiles, ps.up_off, ps.gu, chunks);
+    TS_CHECK_LAUNCH("decode_step_pack launch");
     return TS_OK;
 }
 
@@ -936,8 +951,10 @@ int decode_step_launch(const DecodeStepArgs *a, void *stream) {
         attr = true;
     }
     DecodeStepArgs args = *a;
+    if (!plan_roles(a->H, a->Hq, a->Hkv, a->F, a->NG, args.role_first, args.role_count))
+        return fail(TS_ERR_ARG, "decode_step: %u groups cannot hold this shape", a->NG);
     void *params[] = {&args};
-    hipError_t e = hipLaunchCooperativeKernel((const void *)decode_step_kernel, dim3(a->NG), dim3(kThreads), params,
+    hipError_t e = hipLaunchCooperativeKernel((const void *)decode_step_kernel, dim3(a->NG), dim3(kT), params,
                                               kLdsBytes, (hipStream_t)stream);
     if (e != hipSuccess) return hip_status(e, "decode_step: cooperative launch");
     return TS_OK;

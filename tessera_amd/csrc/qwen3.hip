@@ -102,6 +102,8 @@ struct ts_qwen3 {
     bool use_step = false;  // decode runs it (default when it fits)
     uint64_t *hand = nullptr;
     uint32_t *d_error = nullptr;
+    std::vector<uint16_t *> packed;    // the step's packed weights, [layer][qkv, o, gate/up, down]
+    uint16_t *lm_packed = nullptr;     // and its packed lm_head rows
     uint32_t epoch = 1, groups = 0;
     uint64_t *step_marks = nullptr;  // debug: phase stamps of the next persistent launch
     hipEvent_t ev0 = nullptr, ev1 = nullptr;  // around the last decode call's device work
@@ -239,10 +241,11 @@ int launch_step(ts_qwen3 *m, uint32_t steps) {
     memset(&a, 0, sizeof a);
     for (uint32_t l = 0; l < c.layers; l++) {
         const Layer &L = m->layers[l];
-        a.qkv[l] = L.qkv; a.o[l] = L.o; a.gate_up[l] = L.gate_up; a.down[l] = L.down;
         a.ln1[l] = L.ln1; a.ln2[l] = L.ln2; a.q_norm[l] = L.q_norm; a.k_norm[l] = L.k_norm;
         a.k_cache[l] = L.k_cache; a.v_cache[l] = L.v_cache;
+        for (uint32_t r = 0; r < 4; r++) a.packed[l][r] = m->packed[(size_t)l * 4 + r];
     }
+    a.lm_packed = m->lm_packed;
     a.embed = m->embed; a.norm = m->norm; a.rope = m->rope; a.table = m->d_table;
     a.tok = m->d_tok; a.pos = m->d_pos; a.hist = m->d_hist; a.logits = m->logits;
     a.hand = m->hand; a.error = m->d_error; a.marks = m->step_marks;
@@ -373,7 +376,7 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) return fail(ts::hip_status(e, "open upload"));
     m->pool = tessera_kv_new(m->total_pages, c.page);
-    rc = ts::decode_step_supported(H, c.layers, c.heads, c.kv_heads, D, c.ffn, m->kept_pages);
+    rc = ts::decode_step_supported(H, c.layers, c.heads, c.kv_heads, D, c.ffn, c.vocab, m->kept_pages);
     if (rc < 0) return fail(rc);
     if (rc == TS_OK) {
         if ((rc = ts::decode_step_groups(&m->groups))) return fail(rc);
@@ -381,8 +384,32 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
         if ((rc = m->alloc(&m->hand, words)) || (rc = m->alloc(&m->d_error, 1))) return fail(rc);
         e = hipMemsetAsync(m->hand, 0, words * 8, m->stream);
         if (e == hipSuccess) e = hipMemsetAsync(m->d_error, 0, 4, m->stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
         if (e != hipSuccess) return fail(ts::hip_status(e, "open: hand-off words"));
+        // The step reads its own copy of the weights, laid out for its loads (made
+        // once here, after the weights are written; the graph path reads the originals).
+        m->packed.assign((size_t)c.layers * 4, nullptr);
+        for (uint32_t l = 0; l < c.layers; l++) {
+            const Layer &L = m->layers[l];
+            const uint16_t *src[4] = {L.qkv, L.o, L.gate_up, L.down};
+            for (uint32_t r = 0; r < 4; r++) {
+                const size_t n = ts::decode_step_packed_elems(H, c.heads, c.kv_heads, c.ffn, c.vocab, m->groups, r);
+                uint16_t *dst = nullptr;
+                if ((rc = m->alloc(&dst, n)) ||
+                    (rc = ts::decode_step_pack(src[r], dst, H, c.heads, c.kv_heads, c.ffn, c.vocab, m->groups, r,
+                                               m->stream)))
+                    return fail(rc);
+                m->packed[(size_t)l * 4 + r] = dst;
+            }
+        }
+        {
+            const size_t n = ts::decode_step_packed_elems(H, c.heads, c.kv_heads, c.ffn, c.vocab, m->groups, 4);
+            if ((rc = m->alloc(&m->lm_packed, n)) ||
+                (rc = ts::decode_step_pack(m->embed, m->lm_packed, H, c.heads, c.kv_heads, c.ffn, c.vocab, m->groups,
+                                           4, m->stream)))
+                return fail(rc);
+        }
+        e = hipStreamSynchronize(m->stream);
+        if (e != hipSuccess) return fail(ts::hip_status(e, "open: packed weights"));
         m->step_ok = m->use_step = true;
     }
     *out = m;
