@@ -311,23 +311,9 @@ TS_DEV void tile_out(const Ctx &c, f32x4 acc, float *part, uint32_t t) {
 // ---------------------------------------------------------------------------
 TS_DEV void lm_rows(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t, uint32_t tag) {
     const uint32_t H = p.H;
-    {
-        float v[2], gv[2];
-        gains<2>(c, p.norm, H, gv);
-        poll<2>(c, p.hand + (size_t)(p.L - 1) * hd.block + hd.xo, H, tag, v);
-        stage<2>(c, v, H, gv);
-    }
-    mark(p, c, t, p.L, 0);
-    bar();
-    const float inv = norm_inv(c, H, p.eps);
-    const uint16_t *xs = c.xs();
-    c.ph++;
     const Split rows = split(p.V, p.NG, c.g);
     const uint32_t tiles = (rows.count + 15) / 16;
     constexpr int KS = 4;  // k-steps per wave (H <= 1024)
-    u32x4 xb[KS];
-#pragma unroll
-    for (int j = 0; j < KS; j++) xb[j] = x_frag(c, xs, c.wave * KS + j, H);
     float *part = (float *)(c.lds + kLmPartOff) + c.wave * kMaxLm;
     u32x4 a0[KS], a1[KS], a2[KS], a3[KS];
     // The packed lm_head tiles of this group (decode_step_pack, role 4).
@@ -341,15 +327,30 @@ TS_DEV void lm_rows(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t,
             a[j] = ks < KSt ? __builtin_nontemporal_load(blk + c.lane) : u32x4{0, 0, 0, 0};
         }
     };
+    // The first tiles' loads do not need the input: issued before it is polled.
+    if (tiles > 0) load(0, a0);
+    if (tiles > 1) load(1, a1);
+    if (tiles > 2) load(2, a2);
+    {
+        float v[2], gv[2];
+        gains<2>(c, p.norm, H, gv);
+        poll<2>(c, p.hand + (size_t)(p.L - 1) * hd.block + hd.xo, H, tag, v);
+        stage<2>(c, v, H, gv);
+    }
+    mark(p, c, t, p.L, 0);
+    bar();
+    const float inv = norm_inv(c, H, p.eps);
+    const uint16_t *xs = c.xs();
+    c.ph++;
+    u32x4 xb[KS];
+#pragma unroll
+    for (int j = 0; j < KS; j++) xb[j] = x_frag(c, xs, c.wave * KS + j, H);
     auto use = [&](uint32_t ti, const u32x4 (&a)[KS]) {
         f32x4 acc = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < KS; j++) acc = mfma16(as_bf16x8(a[j]), as_bf16x8(xb[j]), acc);
         tile_out(c, acc, part, ti);
     };
-    if (tiles > 0) load(0, a0);
-    if (tiles > 1) load(1, a1);
-    if (tiles > 2) load(2, a2);
     for (uint32_t i = 0; i < tiles; i += 4) {
         if (i + 3 < tiles) load(i + 3, a3);
         use(i, a0);
