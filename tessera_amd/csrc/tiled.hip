@@ -295,11 +295,28 @@ struct Pipe {
     static constexpr int WM = TM / 2, WN = TN / 2, FI = WM / 16, FJ = WN / 16;
     static_assert(NA >= 1 && NB >= 1 && (KD == 32 || KD == 64), "pipe shape");
 
-    // Byte offset of logical chunk c of row r. 128-byte rows: c ^ (r & 7); 64-byte
-    // rows: c ^ ((r >> 1 ^ r >> 3) & 3). Either way the rows one fragment read touches
-    // (16 consecutive rows, one chunk) fall on distinct banks, in groups of 8 or 16 lanes.
-    TS_DEV static uint32_t sw(uint32_t r) { return CPR == 8 ? (r & 7) : (((r >> 1) ^ (r >> 3)) & 3); }
-    TS_DEV static uint32_t at(uint32_t r, uint32_t c) { return r * RB + ((c ^ sw(r)) << 4); }
+    // Byte offset of logical chunk c of row r. 128-byte rows: chunk c ^ (r & 7) of row
+    // r. 64-byte rows: rows pair up in 128-byte lines L = r / 2, and 16-byte unit
+    // u = 4 (r & 1) + c of a line sits at u ^ (L & 7). Either way the 16 rows one
+    // fragment read touches (one chunk each) spread over all banks (measured: no
+    // conflicts; a per-row XOR of 64-byte rows conflicts).
+    TS_DEV static uint32_t at(uint32_t r, uint32_t c) {
+        if (CPR == 8) return r * 128 + ((c ^ (r & 7)) << 4);
+        const uint32_t L = r >> 1, u = (r & 1) * 4 + c;
+        return L * 128 + ((u ^ (L & 7)) << 4);
+    }
+    // The row (within the RPI rows an instruction fills) and logical chunk that lane l
+    // of a load instruction brings: the lane lands at byte 16 l of the instruction's KiB.
+    TS_DEV static void source(uint32_t l, uint32_t &row, uint32_t &chunk) {
+        const uint32_t line = l >> 3, u = (l & 7) ^ line;  // line & 7 == line: 8 lines per KiB
+        if (CPR == 8) {
+            row = line;
+            chunk = u;
+        } else {
+            row = 2 * line + (u >> 2);
+            chunk = u & 3;
+        }
+    }
 };
 
 constexpr uint32_t kBand = 8;  // tile rows per band of the XCD-aware order
@@ -376,9 +393,10 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
     }
     // Element offsets (at k = 0) of the row each of this lane's loads reads, and the
     // logical chunk it fetches: instruction i of the wave fills rows RPI b .. RPI b +
-    // RPI - 1, b = NA wave + i (A) or NB wave + i (B); lane l lands at physical chunk
-    // l % CPR of row l / CPR. Rows past the end read a row that exists (never stored).
-    const uint32_t rl = lane / P::CPR;
+    // RPI - 1, b = NA wave + i (A) or NB wave + i (B). Rows past the end read a row
+    // that exists (never stored).
+    uint32_t rl, lc;
+    P::source(lane, rl, lc);
     uint32_t aoff[P::NA], boff[P::NB];
 #pragma unroll
     for (int i = 0; i < P::NA; i++) {
@@ -390,7 +408,6 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         } else {
             xr = min(m0 + r, p.m - 1);
         }
-        const uint32_t lc = (lane % P::CPR) ^ P::sw(r);
         aoff[i] = xr * p.k + lc * 8;
     }
 #pragma unroll
@@ -405,7 +422,6 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         } else {
             nr = min(n0 + r, p.n - 1);
         }
-        const uint32_t lc = (lane % P::CPR) ^ P::sw(r);
         boff[i] = nr * p.k + lc * 8;
     }
     const uint16_t *xs = (const uint16_t *)p.x;
@@ -598,10 +614,8 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL)) == 0, "tiled: unknown stage bits %#x",
                a->stages);
     TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "tiled: x and w must be 16-byte aligned");
-#ifndef TS_NO_BIG
     const int big = ts::tiled_big_launch(a, stream);
     if (big != 1) return big;
-#endif
     const bool silu = a->stages & TS_AFTER_SILU_MUL;
     TiledParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;
