@@ -249,26 +249,35 @@ def c4(torch):
 
 
 def blocks(torch):
-    """Block-form weights on the m = 1 decode product (q8_0, mxfp8, int4_g32, q4_0: 32 codes a
-    block under one scale): the Qwen3 lm_head (151936 x 1024) and the Llama-3-8B-like
-    gate (14336 x 4096) shapes, HBM-bound. Bytes = packed rows + 4K (x) + 4N (out)."""
+    """Block-form weights on the m = 1 decode product (the seven forms of block.rs:251-291):
+    the Qwen3 lm_head (151936 x 1024) and the Llama-3-8B-like gate (14336 x 4096) shapes,
+    HBM-bound. Bytes = the packed tensor + 4K (x) + 4N (out)."""
     from tessera_amd import rules
-    sizes = {"q8_0": 34, "mxfp8": 33, "int4_g32": 18, "q4_0": 18}
+    # form: (codes a block, bytes a block, scale bytes, head bytes, scale kind)
+    forms = {"q8_0": (32, 34, 2, 0, "f16"), "mxfp8": (32, 33, 1, 0, "e8m0"), "int4_g32": (32, 18, 2, 0, "f16"),
+             "q4_0": (32, 18, 2, 0, "f16"), "nvfp4": (16, 9, 1, 4, "e4m3"), "mxfp4": (32, 17, 1, 0, "e8m0"),
+             "int4_g128": (128, 66, 2, 0, "f16")}
     res, bytes_all, t_all = {}, 0.0, 0.0
     for shape, (K, N) in {"lm_head": (1024, 151936), "gate": (4096, 14336)}.items():
         x = torch.randn((1, K), device="cuda")
-        for form, bb in sizes.items():
-            rb = K // 32 * bb
-            w = torch.randint(0, 256, (N, rb), device="cuda", dtype=torch.uint8)
-            if form != "mxfp8":  # finite f16 scales
-                w.view(N, K // 32, bb)[:, :, 1] = 0x20
+        for form, (B, bb, sb, head, kind) in forms.items():
+            rb = K // B * bb
+            w = torch.randint(0, 256, (head + N * rb,), device="cuda", dtype=torch.uint8)
+            blk = w[head:].view(N, K // B, bb)
+            if kind == "f16":
+                blk[:, :, 1] = 0x20                      # finite f16 scales
+            elif kind == "e8m0":
+                blk[:, :, 0] = 120
             else:
-                w.view(N, K // 32, bb)[:, :, 0] = 120
-                w.view(N, K // 32, bb)[:, :, 1:] &= 0x77  # no NaN codes
+                blk[:, :, 0] &= 0x77                     # no e4m3 NaN scale
+            if form == "mxfp8":
+                blk[:, :, 1:] &= 0x77                    # no e4m3 NaN codes
+            if head:
+                w[:4] = torch.tensor([0, 0, 128, 63], dtype=torch.uint8, device="cuda")  # f32 1.0
             out = torch.empty((1, N), device="cuda")
-            fn = lambda: rules.lanes(x, w, out=out, w_form=form)
+            fn = lambda: rules.lanes(x, w, out=out, w_form=form, rows=N)
             t = _graph_time(torch, fn, launches=20)
-            nb = N * rb + 4 * K + 4 * N
+            nb = head + N * rb + 4 * K + 4 * N
             res[f"{shape}_{form}"] = {"us": round(t * 1e6, 2), "frac": round(nb / t / HBM_PEAK, 4)}
             bytes_all += nb
             t_all += t

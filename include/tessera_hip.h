@@ -34,15 +34,19 @@ extern "C" {
 #define TS_ERR_WORKSPACE (-3) /* workspace missing or too small */
 
 /* Storage types (engine/ir/mem/src/form.rs forms used on this path). The block forms
- * (engine/ir/mem/src/block.rs:258-286) hold each weight row as k/32 blocks, each one
- * scale then 32 codes, rows back to back (k a multiple of 128); w_scale is unused:
- *   TS_Q8_0      34 B a block: f16 scale, 32 signed bytes
- *   TS_MXFP8     33 B a block: e8m0 scale, 32 e4m3 codes
- *   TS_INT4_G32  18 B a block: f16 scale, 32 nibbles (code - 8), element 2q low, 2q+1 high
- *   TS_Q4_0      18 B a block: f16 scale, 32 nibbles (code - 8), element q low, q+16 high
- * They are accepted by tessera_hip_lanes / tessera_hip_linear for m <= 4 rows. */
+ * (engine/ir/mem/src/block.rs:251-291) hold the [n, k] weights as one packed tensor:
+ * an optional 4-byte f32 head, then k/B blocks per row, each one scale then B codes,
+ * rows back to back (k a multiple of 4 B and at least 128); w_scale is unused:
+ *   TS_Q8_0       34 B a block: f16 scale, 32 signed bytes
+ *   TS_MXFP8      33 B a block: e8m0 scale, 32 e4m3 codes
+ *   TS_INT4_G32   18 B a block: f16 scale, 32 nibbles (code - 8), element 2q low, 2q+1 high
+ *   TS_Q4_0       18 B a block: f16 scale, 32 nibbles (code - 8), element q low, q+16 high
+ *   TS_NVFP4       9 B a block: e4m3 scale, 16 e2m1 nibbles (2q low, 2q+1 high); f32 head
+ *   TS_MXFP4      17 B a block: e8m0 scale, 32 e2m1 nibbles (2q low, 2q+1 high)
+ *   TS_INT4_G128  66 B a block: f16 scale, 128 nibbles (code - 8), 2q low, 2q+1 high
+ * tessera_hip_lanes / tessera_hip_linear / tessera_hip_tiled accept them at any m. */
 enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 = 5, TS_INT4_G32 = 6,
-       TS_Q4_0 = 7 };
+       TS_Q4_0 = 7, TS_NVFP4 = 8, TS_MXFP4 = 9, TS_INT4_G128 = 10 };
 
 /* Fused stages around a product (engine/plan/lower/src/kernels/map.rs:20-59 MapStage,
  * applied by `finish` at the store, map.rs:155-185). */

@@ -79,9 +79,15 @@ def lib():
         "or_e8m0_narrow": (C.c_uint8, [C.c_float]),
         "or_e8m0_widen": (C.c_float, [C.c_uint8]),
         "or_block_bytes": (C.c_int, [C.c_int]),
+        "or_block_size": (C.c_int, [C.c_int]),
+        "or_block_head": (C.c_int, [C.c_int]),
+        "or_block_tensor_bytes": (_i64, [C.c_int, _i64]),
+        "or_e2m1_narrow": (C.c_uint8, [C.c_float]),
+        "or_e2m1_widen": (C.c_float, [C.c_uint8]),
         "or_block_pack": (None, [C.c_int, _f32p, _i64, _u8p]),
         "or_block_unpack": (C.c_float, [C.c_int, _u8p, _i64]),
-        "or_block_dot": (C.c_float, [C.c_int, _f32p, _u8p, _i64]),
+        "or_block_unpack_n": (None, [C.c_int, _u8p, _i64, _i64, _f32p]),
+        "or_block_dot": (C.c_float, [C.c_int, _f32p, _u8p, _i64, _i64]),
         "or_block_product": (None, [C.c_int, _i64, _i64, _i64, _f32p, _u8p, _f32p]),
     }
     for name, (res, args) in sig.items():
@@ -335,43 +341,51 @@ def mix(x, weights=None) -> np.ndarray:
 
 
 # --- block forms: engine/ir/mem/src/block.rs:1-291 --------------------------------
-# Each form: 32 codes after one scale per block, no head. Rows of a [n, k] matrix are
-# packed one after another (k a multiple of 32, so blocks never straddle rows).
-BLOCK_FORMS = {"q8_0": 0, "mxfp8": 1, "int4_g32": 2, "q4_0": 3}
+# A packed tensor is [head] then its blocks in element order; a [n, k] matrix (k a
+# multiple of the block) has row r's blocks from head + r k / B block bytes on.
+BLOCK_FORMS = {"q8_0": 0, "mxfp8": 1, "int4_g32": 2, "q4_0": 3, "nvfp4": 4, "mxfp4": 5, "int4_g128": 6}
 
 
 def block_bytes(form: str) -> int:
+    """Bytes of one block (scale and codes)."""
     return lib().or_block_bytes(BLOCK_FORMS[form])
 
 
-def block_pack(form: str, w) -> np.ndarray:
-    """Packs each row of w [n, k] (k % 32 == 0) into [n, k / 32 * block_bytes] bytes."""
-    w = _f32(np.atleast_2d(w))
-    n, k = w.shape
-    assert k % 32 == 0
-    rb = k // 32 * block_bytes(form)
-    out = np.zeros((n, rb), np.uint8)
-    for r in range(n):
-        lib().or_block_pack(BLOCK_FORMS[form], w[r], k, out[r])
+def block_size(form: str) -> int:
+    return lib().or_block_size(BLOCK_FORMS[form])
+
+
+def block_head(form: str) -> int:
+    return lib().or_block_head(BLOCK_FORMS[form])
+
+
+def block_pack(form: str, data) -> np.ndarray:
+    """Packs data (any shape, flattened in C order) as one tensor: uint8 [bytes(n)]."""
+    d = _f32(np.ravel(data))
+    out = np.zeros(lib().or_block_tensor_bytes(BLOCK_FORMS[form], d.size), np.uint8)
+    lib().or_block_pack(BLOCK_FORMS[form], d, d.size, out)
     return out
 
 
-def block_unpack(form: str, bytes_row: np.ndarray, k: int) -> np.ndarray:
-    b = np.ascontiguousarray(bytes_row, dtype=np.uint8)
-    return np.array([lib().or_block_unpack(BLOCK_FORMS[form], b, i) for i in range(k)], np.float32)
+def block_unpack(form: str, tensor: np.ndarray, count: int, first: int = 0) -> np.ndarray:
+    """Elements first .. first + count of a packed tensor."""
+    b = np.ascontiguousarray(tensor, dtype=np.uint8)
+    out = np.empty(count, np.float32)
+    lib().or_block_unpack_n(BLOCK_FORMS[form], b, first, count, out)
+    return out
 
 
-def block_dot(form: str, x, bytes_row) -> float:
+def block_dot(form: str, x, tensor, at: int = 0) -> float:
+    """Block::dot: x against the tensor's elements from `at` (a block start) on."""
     x = _f32(x)
-    return lib().or_block_dot(BLOCK_FORMS[form], x, np.ascontiguousarray(bytes_row, dtype=np.uint8), x.size)
+    return lib().or_block_dot(BLOCK_FORMS[form], x, np.ascontiguousarray(tensor, dtype=np.uint8), at, x.size)
 
 
-def block_product(form: str, x, wb) -> np.ndarray:
-    """out[m, r] = dot(x[m], packed row r), the reference's Block::dot per output."""
+def block_product(form: str, x, wb, n: int) -> np.ndarray:
+    """out[m, r] = dot(x[m], the packed [n, k] tensor from element r k), per output."""
     x = _f32(np.atleast_2d(x))
     wb = np.ascontiguousarray(wb, dtype=np.uint8)
     m, k = x.shape
-    n = wb.shape[0]
     out = np.empty((m, n), np.float32)
     lib().or_block_product(BLOCK_FORMS[form], m, n, k, x, wb.reshape(-1), out)
     return out

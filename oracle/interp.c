@@ -22,9 +22,12 @@
  *   paged row                     closed form of kept.rs Paged::row
  *   f16, e8m0                     exhaustive f16 code round trips, numpy's RNE float16
  *                                 on random f32, e8m0 round-up closed forms
- *   block pack / dot              blocks_round_trip of block_test.rs (byte counts,
- *                                 round-trip share, dot == sum over unpacked), hand-built
- *                                 blocks with closed-form sums, code placement by form
+ *   e2m1                          the 16-code table, ties-to-even-code rounding on a
+ *                                 dense grid (brute-force nearest), saturation
+ *   block pack / dot              blocks_round_trip of block_test.rs for all seven forms
+ *                                 (byte counts, round-trip share, dot == sum over
+ *                                 unpacked), hand-built blocks with closed-form sums,
+ *                                 code placement by form, the nvfp4 head, e8m0 round-up
  */
 #include <math.h>
 #include <stdint.h>
@@ -127,36 +130,64 @@ EXPORT float or_e8m0_widen(uint8_t e) { return e == 0xFF ? NAN : (float)pow2d((i
 /* ------------------------------------------------------------------ */
 /* Block forms: engine/ir/mem/src/block.rs:1-291                       */
 /* ------------------------------------------------------------------ */
-/* form 0 = q8_0 (F16 scale, I8 codes, halves), 1 = mxfp8 (E8M0 scale, E4M3 codes),
- * 2 = int4_g32 (F16 scale, Nibble codes, adjacent pairs), 3 = q4_0 (F16 scale, Nibble
- * codes paired by halves); 32 codes a block, no head. */
-static int blk_scale_bytes(int form) { return form == 1 ? 1 : 2; }
-static int blk_bits(int form) { return form >= 2 ? 4 : 8; }
-EXPORT int or_block_bytes(int form) { return blk_scale_bytes(form) + 32 * blk_bits(form) / 8; }
+/* The seven forms of block.rs:251-291, by id:
+ *   0 q8_0      F16 scale,  I8 codes,     32 a block, halves
+ *   1 mxfp8     E8M0 scale, E4M3 codes,   32
+ *   2 int4_g32  F16 scale,  Nibble codes, 32, adjacent pairs
+ *   3 q4_0      F16 scale,  Nibble codes, 32, halves
+ *   4 nvfp4     E4M3 scale, E2M1 codes,   16, adjacent pairs, f32 head
+ *   5 mxfp4     E8M0 scale, E2M1 codes,   32, adjacent pairs
+ *   6 int4_g128 F16 scale,  Nibble codes, 128, adjacent pairs
+ * A tensor is [head] then its blocks, in element order (a [n, k] matrix with k a
+ * multiple of the block: row r's blocks start at head + r k / B block bytes). */
+enum { SC_F16, SC_E8M0, SC_E4M3 };
+enum { CD_I8, CD_E4M3, CD_NIB, CD_E2M1 };
+typedef struct { int scale, code, B, halves, head; } BlkSpec;
+static const BlkSpec kForms[7] = {
+    {SC_F16, CD_I8, 32, 1, 0},   {SC_E8M0, CD_E4M3, 32, 0, 0}, {SC_F16, CD_NIB, 32, 0, 0},
+    {SC_F16, CD_NIB, 32, 1, 0},  {SC_E4M3, CD_E2M1, 16, 0, 1}, {SC_E8M0, CD_E2M1, 32, 0, 0},
+    {SC_F16, CD_NIB, 128, 0, 0},
+};
+static int blk_scale_bytes(int form) { return kForms[form].scale == SC_F16 ? 2 : 1; }
+static int blk_bits(int form) { return kForms[form].code <= CD_E4M3 ? 8 : 4; }
+EXPORT int or_block_size(int form) { return kForms[form].B; }
+EXPORT int or_block_head(int form) { return kForms[form].head ? 4 : 0; }
+EXPORT int or_block_bytes(int form) { return blk_scale_bytes(form) + kForms[form].B * blk_bits(form) / 8; }
+EXPORT int64_t or_block_tensor_bytes(int form, int64_t n) {
+    const int B = kForms[form].B;
+    return or_block_head(form) + (n + B - 1) / B * or_block_bytes(form);
+}
 
-/* place (block.rs:131-137): 8-bit codes at byte j; nibbles paired by halves (j % 16,
- * shift 4 (j / 16)) or adjacent (j / 2, shift 4 (j % 2)). */
+/* E2M1 (scalar.rs:132-135): 2 exponent bits, 1 mantissa bit, no inf, no NaN. */
+EXPORT uint8_t or_e2m1_narrow(float x) { return (uint8_t)narrow_fmt(x, 2, 1, 0, 0); }
+EXPORT float or_e2m1_widen(uint8_t b) { return widen_fmt(b & 15u, 2, 1, 0, 0); }
+
+/* place (block.rs:131-137): 8-bit codes at byte j; nibbles paired by halves (j % (B/2),
+ * shift 4 (j / (B/2))) or adjacent (j / 2, shift 4 (j % 2)). */
 static void blk_place(int form, int j, int *byte, int *shift) {
+    const BlkSpec *f = &kForms[form];
     if (blk_bits(form) == 8) { *byte = j; *shift = 0; return; }
-    if (form == 3) { *byte = j % 16; *shift = 4 * (j / 16); return; } /* q4_0: halves = true */
-    *byte = j / 2; *shift = 4 * (j % 2);                              /* int4_g32: halves = false */
+    if (f->halves) { *byte = j % (f->B / 2); *shift = 4 * (j / (f->B / 2)); return; }
+    *byte = j / 2; *shift = 4 * (j % 2);
 }
 static float blk_decode(int form, uint32_t code) {
-    switch (form) {
-    case 0: return (float)(int8_t)(uint8_t)code;          /* I8 (block.rs:79-90) */
-    case 1: return or_e4m3_widen((uint8_t)code);           /* E4M3 (block.rs:66-76) */
-    default: return (float)code - 8.0f;                    /* Nibble (block.rs:95-104), q4_0 and int4_g32 */
+    switch (kForms[form].code) {
+    case CD_I8: return (float)(int8_t)(uint8_t)code;      /* I8 (block.rs:79-90) */
+    case CD_E4M3: return or_e4m3_widen((uint8_t)code);     /* E4M3 (block.rs:66-76) */
+    case CD_E2M1: return or_e2m1_widen((uint8_t)code);     /* E2M1 (block.rs:49-63) */
+    default: return (float)code - 8.0f;                    /* Nibble (block.rs:95-104) */
     }
 }
 static uint32_t blk_encode(int form, float scaled) {
-    switch (form) {
-    case 0: { /* round_ties_even, clamp to [-128, 127], as a byte */
+    switch (kForms[form].code) {
+    case CD_I8: { /* round_ties_even, clamp to [-128, 127], as a byte */
         float r = nearbyintf(scaled);
         r = r < -128.0f ? -128.0f : (r > 127.0f ? 127.0f : r);
         if (isnan(scaled)) r = 0.0f; /* Rust's saturating cast: NaN -> 0 */
         return (uint32_t)(uint8_t)(int8_t)r;
     }
-    case 1: return or_e4m3_narrow(scaled);
+    case CD_E4M3: return or_e4m3_narrow(scaled);
+    case CD_E2M1: return or_e2m1_narrow(scaled);
     default: { /* (scaled + 8.5).clamp(0, 15) as u32: truncation */
         float t = scaled + 8.5f;
         t = t < 0.0f ? 0.0f : (t > 15.0f ? 15.0f : t);
@@ -165,38 +196,68 @@ static uint32_t blk_encode(int form, float scaled) {
     }
     }
 }
-/* Code::scale (block.rs:15-17) and Nibble::scale (block.rs:107-113). */
+/* Code::scale (block.rs:15-17: widest magnitude over the code's MAX) and
+ * Nibble::scale (block.rs:107-113: the widest value, sign kept, over -8). */
 static float blk_code_scale(int form, const float *b, int n) {
-    if (form >= 2) {
+    const int code = kForms[form].code;
+    if (code == CD_NIB) {
         float top = 0.0f;
         for (int i = 0; i < n; i++) if (fabsf(b[i]) > fabsf(top)) top = b[i];
         return top / -8.0f;
     }
     float m = 0.0f;
     for (int i = 0; i < n; i++) m = fmaxf(m, fabsf(b[i]));
-    return m / (form == 0 ? 127.0f : 448.0f);
+    return m / (code == CD_I8 ? 127.0f : code == CD_E4M3 ? 448.0f : 6.0f);
 }
 static void blk_put(int form, float scale, uint8_t *at) {
-    if (form == 1) { at[0] = or_e8m0_narrow(scale); return; }
-    uint16_t h = or_f16_narrow(scale);
-    at[0] = (uint8_t)h; at[1] = (uint8_t)(h >> 8);
+    switch (kForms[form].scale) {
+    case SC_E8M0: at[0] = or_e8m0_narrow(scale); return;
+    case SC_E4M3: at[0] = or_e4m3_narrow(scale); return;
+    default: {
+        uint16_t h = or_f16_narrow(scale);
+        at[0] = (uint8_t)h; at[1] = (uint8_t)(h >> 8);
+    }
+    }
 }
 static float blk_get(int form, const uint8_t *at) {
-    if (form == 1) return or_e8m0_widen(at[0]);
-    return or_f16_widen((uint16_t)(at[0] | (at[1] << 8)));
+    switch (kForms[form].scale) {
+    case SC_E8M0: return or_e8m0_widen(at[0]);
+    case SC_E4M3: return or_e4m3_widen(at[0]);
+    default: return or_f16_widen((uint16_t)(at[0] | (at[1] << 8)));
+    }
+}
+/* head (block.rs:141-146): the f32 at the tensor's start, else 1.0. */
+static float blk_head(int form, const uint8_t *bytes) {
+    if (!kForms[form].head) return 1.0f;
+    float h;
+    memcpy(&h, bytes, 4);
+    return h;
 }
 
-/* pack (block.rs:229-248): per block, the scale from its values, stored; codes are
- * the values over the scale as stored (0 when it is 0). `out` must be zeroed. */
+/* pack (block.rs:229-248, tensor_scale :148-158): the head is the widest block scale
+ * over the scale type's MAX (E4M3: 448) when the form has one and it is not 0; each
+ * block's scale is its code scale over the head, stored; codes are the values over
+ * the stored scale times the head (0 when that is 0). `out` must be zeroed. */
 EXPORT void or_block_pack(int form, const float *data, int64_t n, uint8_t *out) {
-    const int bb = or_block_bytes(form), sb = blk_scale_bytes(form);
-    for (int64_t b = 0; b * 32 < n; b++) {
-        const int cnt = (int)(n - b * 32 < 32 ? n - b * 32 : 32);
-        uint8_t *at = out + b * bb;
-        blk_put(form, blk_code_scale(form, data + b * 32, cnt), at);
-        const float stored = blk_get(form, at);
+    const BlkSpec *f = &kForms[form];
+    const int B = f->B, bb = or_block_bytes(form), sb = blk_scale_bytes(form), hb = or_block_head(form);
+    float tensor = 1.0f;
+    if (f->head) {
+        float widest = 0.0f;
+        for (int64_t b = 0; b * B < n; b++) {
+            const int cnt = (int)(n - b * B < B ? n - b * B : B);
+            widest = fmaxf(widest, fabsf(blk_code_scale(form, data + b * B, cnt)));
+        }
+        if (widest > 0.0f) tensor = widest / 448.0f;
+        memcpy(out, &tensor, 4);
+    }
+    for (int64_t b = 0; b * B < n; b++) {
+        const int cnt = (int)(n - b * B < B ? n - b * B : B);
+        uint8_t *at = out + hb + b * bb;
+        blk_put(form, blk_code_scale(form, data + b * B, cnt) / tensor, at);
+        const float stored = blk_get(form, at) * tensor;
         for (int j = 0; j < cnt; j++) {
-            const float scaled = stored == 0.0f ? 0.0f : data[b * 32 + j] / stored;
+            const float scaled = stored == 0.0f ? 0.0f : data[b * B + j] / stored;
             int byte, shift;
             blk_place(form, j, &byte, &shift);
             at[sb + byte] |= (uint8_t)(blk_encode(form, scaled) << shift);
@@ -204,43 +265,51 @@ EXPORT void or_block_pack(int form, const float *data, int64_t n, uint8_t *out) 
     }
 }
 
-/* unpack (block.rs:221-227). */
+/* unpack (block.rs:219-225): head * scale * decode(code) for element `index`. */
 EXPORT float or_block_unpack(int form, const uint8_t *bytes, int64_t index) {
-    const uint8_t *at = bytes + (index / 32) * or_block_bytes(form);
+    const int B = kForms[form].B;
+    const uint8_t *at = bytes + or_block_head(form) + (index / B) * or_block_bytes(form);
     int byte, shift;
-    blk_place(form, (int)(index % 32), &byte, &shift);
+    blk_place(form, (int)(index % B), &byte, &shift);
     const uint32_t code = ((uint32_t)at[blk_scale_bytes(form) + byte] >> shift) & ((1u << blk_bits(form)) - 1);
-    return blk_get(form, at) * blk_decode(form, code);
+    const float sw = blk_get(form, at) * blk_decode(form, code);
+    return blk_head(form, bytes) * sw;
 }
 
-/* dot (block.rs:202-219): per block, part = sum_j x_j decode(c_j) from 0.0 in j order;
- * sum += scale * part in block order; times the head (1.0 for these forms). */
-EXPORT float or_block_dot(int form, const float *x, const uint8_t *bytes, int64_t n) {
-    const int bb = or_block_bytes(form), sb = blk_scale_bytes(form);
+EXPORT void or_block_unpack_n(int form, const uint8_t *bytes, int64_t first, int64_t count, float *out) {
+    for (int64_t i = 0; i < count; i++) out[i] = or_block_unpack(form, bytes, first + i);
+}
+
+/* dot (block.rs:202-217): from element `at` (a block start) of the tensor, per block
+ * part = sum_j x_j decode(c_j) from 0.0 in j order; sum += scale * part in block
+ * order; the head times the sum. */
+EXPORT float or_block_dot(int form, const float *x, const uint8_t *bytes, int64_t at, int64_t n) {
+    const int B = kForms[form].B, bb = or_block_bytes(form), sb = blk_scale_bytes(form);
     const uint32_t mask = (1u << blk_bits(form)) - 1;
+    const float head = blk_head(form, bytes);
     float sum = 0.0f;
-    for (int64_t b = 0; b * 32 < n; b++) {
-        const uint8_t *at = bytes + b * bb;
+    for (int64_t b = 0; b * B < n; b++) {
+        const uint8_t *blk = bytes + or_block_head(form) + (at / B + b) * bb;
         float part = 0.0f;
-        for (int j = 0; j < 32 && b * 32 + j < n; j++) {
+        for (int j = 0; j < B && b * B + j < n; j++) {
             int byte, shift;
             blk_place(form, j, &byte, &shift);
-            const float prod = x[b * 32 + j] * blk_decode(form, ((uint32_t)at[sb + byte] >> shift) & mask);
+            const float prod = x[b * B + j] * blk_decode(form, ((uint32_t)blk[sb + byte] >> shift) & mask);
             part = part + prod;
         }
-        const float sp = blk_get(form, at) * part;
+        const float sp = blk_get(form, blk) * part;
         sum = sum + sp;
     }
-    return 1.0f * sum;
+    return head * sum;
 }
 
-/* out[m, r] = dot(x[m], row r) for rows packed one after another (k a multiple of 32). */
+/* out[m, r] = dot(x[m], the tensor from element r k) for a [n, k] tensor (k a multiple
+ * of the block). */
 EXPORT void or_block_product(int form, int64_t m, int64_t n, int64_t k, const float *x, const uint8_t *w,
                              float *out) {
-    const int64_t rb = k / 32 * or_block_bytes(form);
 #pragma omp parallel for num_threads(g_threads) schedule(static)
     for (int64_t r = 0; r < n; r++)
-        for (int64_t i = 0; i < m; i++) out[i * n + r] = or_block_dot(form, x + i * k, w + r * rb, k);
+        for (int64_t i = 0; i < m; i++) out[i * n + r] = or_block_dot(form, x + i * k, w, r * k, k);
 }
 
 EXPORT void or_bf16_narrow_n(const float *x, uint16_t *out, int64_t n) {

@@ -23,7 +23,8 @@ TS_ERR_WORKSPACE = -3
 TS_STATUS_POSITION = 1  # ts_rows_args.status: a row's position was refused
 
 TS_F32, TS_BF16, TS_E4M3, TS_U32 = 0, 1, 2, 3
-TS_Q8_0, TS_MXFP8, TS_INT4_G32, TS_Q4_0 = 4, 5, 6, 7  # block forms (engine/ir/mem/src/block.rs:258-286)
+TS_Q8_0, TS_MXFP8, TS_INT4_G32, TS_Q4_0 = 4, 5, 6, 7  # block forms (engine/ir/mem/src/block.rs:251-291)
+TS_NVFP4, TS_MXFP4, TS_INT4_G128 = 8, 9, 10
 
 TS_AFTER_ADD = 1
 TS_AFTER_SILU_MUL = 2

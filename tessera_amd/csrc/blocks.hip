@@ -1,34 +1,32 @@
-// Block-scaled weight forms on the decode product (m <= 4 rows): q8_0, mxfp8,
-// int4_g32 and q4_0, each 32 codes under one narrow scale.
+// Block-scaled weight forms on the decode product (m <= 4 rows): the reference's
+// seven block forms (q8_0, mxfp8, int4_g32, q4_0, nvfp4, mxfp4, int4_g128).
 //
 // Replaces the decode of a block form inside the few-row product: the reference's
-// Block::dot (engine/ir/mem/src/block.rs:202-219) with the forms Q8_0 (f16 scale,
-// signed bytes), MXFP8 (e8m0 scale, e4m3 codes) and INT4_G32 (f16 scale, nibbles
-// 8 below their value, adjacent pairs per byte) and Q4_0 (the same nibbles paired
-// by halves: element j in byte j % 16, high nibble for j >= 16), block.rs:258-286, as the lanes
-// rule reads them through a form's load (engine/plan/codegen/src/form.rs:10-93).
+// Block::dot (engine/ir/mem/src/block.rs:202-217) over the forms of block.rs:251-291,
+// as the lanes rule reads them through a form's load (engine/plan/codegen/src/
+// form.rs:10-93). blockform.h holds each form's layout and exact decode.
 //
-// gfx950 design. One wave per 4 weight rows. A row is K/32 blocks of 33, 34 or 18
-// bytes, so blocks are not 16-byte aligned: the wave streams its rows' bytes with
-// coalesced 4-byte loads (all four rows in flight together) into its own LDS
-// slices, 64 blocks at a time, and lane l then decodes block l of each row. Each lane forms its block's part in the
-// reference's order (x_j times the decoded code, summed from 0.0 in j order, no
-// contraction), times the block scale; lane (row, m) then adds the contributions of
-// activation row m in block order. Every rounding step is the reference's, so the
-// product is bit-identical to Block::dot for the same f32 activations.
-#include "common.h"
+// gfx950 design. One wave per 4 weight rows. Blocks are 9 to 66 bytes, not 16-byte
+// aligned: the wave streams its rows' bytes with coalesced 4-byte loads (all four rows
+// in flight together) into its own LDS slices, one block per lane (64 blocks a slice;
+// 16 of the 128-code blocks), and lane l then decodes block l of each row. Each lane
+// forms its block's part in the reference's order (x_j times the decoded code, summed
+// from 0.0 in j order, no contraction), times the block scale; lane (row, m) then adds
+// the contributions of activation row m in block order, and the head (nvfp4) scales
+// the total. Every rounding step is the reference's, so the product is bit-identical
+// to Block::dot for the same f32 activations.
+#include "blockform.h"
 
 namespace ts {
 
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kChunk = 64;  // blocks per LDS slice: one per lane
 constexpr int kRows = 4;    // weight rows per wave, their loads overlapped
 
 struct BlockParams {
     const void *x;
-    const uint8_t *w;
+    const uint8_t *w;  // the packed tensor (head included)
     const float *a0;
     void *out;
     uint32_t m, n, k;
@@ -36,23 +34,9 @@ struct BlockParams {
     int out_bf16;
 };
 
-// FORM: 0 q8_0, 1 mxfp8, 2 int4_g32, 3 q4_0.
-template <int FORM>
-struct Form {
-    static constexpr int kScaleBytes = FORM == 1 ? 1 : 2;
-    static constexpr int kBytes = kScaleBytes + (FORM >= 2 ? 16 : 32);
-};
-
-// f16 scale, little-endian (exact widening, subnormals included).
-TS_DEV float f16_value(uint32_t lo, uint32_t hi) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(lo | (hi << 8)));
-}
-
-// e8m0 scale: 2^(e - 127); 0xFF is NaN (engine/ir/graph/src/scalar.rs:154-161).
-TS_DEV float e8m0_value(uint32_t e) {
-    if (e == 0xFF) return __uint_as_float(0x7fc00000u);
-    return e == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(e << 23);
-}
+// Blocks per LDS slice: one per lane (16 for 128-code blocks, keeping the slice small).
+template <int F>
+constexpr int chunk_blocks() { return BlockForm<F>::B == 128 ? 16 : 64; }
 
 // Waits for this wave's LDS traffic so the other lanes' writes are visible.
 TS_DEV void wave_lds_sync() {
@@ -62,29 +46,57 @@ TS_DEV void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-template <int FORM, int M, bool XF32>
+// x[k0 .. k0 + P) of one row as f32 (exact for bf16 rows).
+template <int P, bool XF32>
+TS_DEV void load_x(const void *x, size_t at, float *xv) {
+    if (XF32) {
+        const float4 *xs = (const float4 *)((const float *)x + at);
+#pragma unroll
+        for (int q = 0; q < P / 4; q++) {
+            const float4 t = xs[q];
+            xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
+        }
+    } else {
+        const u32x4 *xs = (const u32x4 *)((const uint16_t *)x + at);
+#pragma unroll
+        for (int q = 0; q < P / 8; q++) {
+            const u32x4 t = xs[q];
+            const uint32_t u[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xv[8 * q + 2 * e] = lo_bf16(u[e]);
+                xv[8 * q + 2 * e + 1] = hi_bf16(u[e]);
+            }
+        }
+    }
+}
+
+template <int F, int M, bool XF32>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) {
 #pragma clang fp contract(off)
-    constexpr int SB = Form<FORM>::kScaleBytes, BB = Form<FORM>::kBytes;
-    constexpr int kSlice = kChunk * BB / 4;                 // words of one row's slice
-    constexpr int kWords = (kSlice + 63) / 64;              // of them per lane (at most 9)
+    using BF = BlockForm<F>;
+    constexpr int B = BF::B, BB = BF::BB, SB = BF::SB, CH = chunk_blocks<F>();
+    constexpr int P = B < 32 ? B : 32;                   // elements decoded per piece
+    constexpr int kSlice = CH * BB / 4;                  // words of one row's slice
+    constexpr int kWords = (kSlice + 63) / 64;           // of them per lane
     __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kRows][kSlice];
-    __shared__ __attribute__((aligned(16))) float contrib[kWaves][kRows * M][kChunk];
+    __shared__ __attribute__((aligned(16))) float contrib[kWaves][kRows * M][CH];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t r0 = (blockIdx.x * kWaves + wave) * kRows;  // this wave's kRows rows
     if (r0 >= p.n) return;  // waves are independent: no group barrier below
-    const uint32_t K = p.k, N = p.n, Mr = p.m, nb = K / 32;
+    const uint32_t K = p.k, N = p.n, Mr = p.m, nb = K / B;
     const uint32_t nrows = min((uint32_t)kRows, N - r0);
+    const uint8_t *rows = p.w + BF::HEAD;
 
     float run = 0.0f;  // lane rr * M + m: the running sum of output (m, r0 + rr)
-    for (uint32_t c0 = 0; c0 < nb; c0 += kChunk) {
-        const uint32_t cnt = min((uint32_t)kChunk, nb - c0), words = cnt * BB / 4;
+    for (uint32_t c0 = 0; c0 < nb; c0 += CH) {
+        const uint32_t cnt = min((uint32_t)CH, nb - c0), words = cnt * BB / 4;
         // Every word of the rows' slices in flight before any is written.
         uint32_t wt[kRows][kWords];
 #pragma unroll
         for (int rr = 0; rr < kRows; rr++) {
-            const uint32_t *src = (const uint32_t *)(p.w + (size_t)(r0 + min((uint32_t)rr, nrows - 1)) * nb * BB) +
+            const uint32_t *src = (const uint32_t *)(rows + (size_t)(r0 + min((uint32_t)rr, nrows - 1)) * nb * BB) +
                                   (size_t)c0 * BB / 4;
 #pragma unroll
             for (int q = 0; q < kWords; q++) {
@@ -99,76 +111,40 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
                 if (lane + 64 * q < words) stage[wave][rr][lane + 64 * q] = wt[rr][q];
         wave_lds_sync();
         if (lane < cnt) {
-            const uint32_t k0 = (c0 + lane) * 32;
+            const uint32_t k0 = (c0 + lane) * B;
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 if ((uint32_t)m >= Mr) break;
-                float xv[32];
-                if (XF32) {
-                    const float4 *xs = (const float4 *)((const float *)p.x + (size_t)m * K + k0);
+                float part[kRows];
 #pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        const float4 t = xs[q];
-                        xv[4 * q] = t.x; xv[4 * q + 1] = t.y; xv[4 * q + 2] = t.z; xv[4 * q + 3] = t.w;
-                    }
-                } else {
-                    const u32x4 *xs = (const u32x4 *)((const uint16_t *)p.x + (size_t)m * K + k0);
+                for (int rr = 0; rr < kRows; rr++) part[rr] = 0.0f;
+                // Block::dot's part: x_j times code j, summed from 0.0 in j order.
+#pragma unroll 1
+                for (int q = 0; q < B / P; q++) {
+                    float xv[P];
+                    load_x<P, XF32>(p.x, (size_t)m * K + k0 + q * P, xv);
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const u32x4 t = xs[q];
-                        const uint32_t u[4] = {t.x, t.y, t.z, t.w};
+                    for (int rr = 0; rr < kRows; rr++) {
+                        const uint8_t *codes = (const uint8_t *)stage[wave][rr] + lane * BB + SB;
 #pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            xv[8 * q + 2 * e] = lo_bf16(u[e]);
-                            xv[8 * q + 2 * e + 1] = hi_bf16(u[e]);
-                        }
+                        for (int j = 0; j < P; j++) part[rr] = part[rr] + xv[j] * block_code<F>(codes, q * P + j);
                     }
                 }
 #pragma unroll
                 for (int rr = 0; rr < kRows; rr++) {
                     const uint8_t *blk = (const uint8_t *)stage[wave][rr] + lane * BB;
-                    const float scale = FORM == 1 ? e8m0_value(blk[0]) : f16_value(blk[0], blk[1]);
-                    float wv[32];
-                    if (FORM == 0) {
-#pragma unroll
-                        for (int j = 0; j < 32; j++) wv[j] = (float)(int8_t)blk[SB + j];
-                    } else if (FORM == 1) {
-#pragma unroll
-                        for (int q = 0; q < 8; q++) {
-                            const uint32_t c = blk[SB + 4 * q] | (blk[SB + 4 * q + 1] << 8) |
-                                               (blk[SB + 4 * q + 2] << 16) | ((uint32_t)blk[SB + 4 * q + 3] << 24);
-                            e4m3x4_to_f32(c, wv + 4 * q);
-                        }
-                    } else if (FORM == 2) {  // adjacent pairs: element 2q low, 2q + 1 high
-#pragma unroll
-                        for (int q = 0; q < 16; q++) {
-                            const uint32_t b = blk[SB + q];
-                            wv[2 * q] = (float)(b & 15u) - 8.0f;
-                            wv[2 * q + 1] = (float)(b >> 4) - 8.0f;
-                        }
-                    } else {  // halves: element q low, q + 16 high
-#pragma unroll
-                        for (int q = 0; q < 16; q++) {
-                            const uint32_t b = blk[SB + q];
-                            wv[q] = (float)(b & 15u) - 8.0f;
-                            wv[q + 16] = (float)(b >> 4) - 8.0f;
-                        }
-                    }
-                    float part = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 32; j++) part = part + xv[j] * wv[j];
-                    contrib[wave][rr * M + m][lane] = scale * part;
+                    contrib[wave][rr * M + m][lane] = block_scale<F>(blk) * part[rr];
                 }
             }
         }
         wave_lds_sync();
-        if (lane < kRows * M) {  // all 64 contributions read first, then added in block order
+        if (lane < kRows * M) {  // all contributions read first, then added in block order
             const float4 *cv = (const float4 *)contrib[wave][lane];
-            float4 t[kChunk / 4];
+            float4 t[CH / 4];
 #pragma unroll
-            for (int q = 0; q < kChunk / 4; q++) t[q] = cv[q];
+            for (int q = 0; q < CH / 4; q++) t[q] = cv[q];
 #pragma unroll
-            for (int q = 0; q < kChunk / 4; q++)
+            for (int q = 0; q < CH / 4; q++)
                 if ((uint32_t)(4 * q) < cnt) {  // cnt is a multiple of 4
                     run = run + t[q].x;
                     run = run + t[q].y;
@@ -180,7 +156,8 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
     }
     const uint32_t rr = lane / M, m = lane % M;
     if (lane >= kRows * M || rr >= nrows || m >= Mr) return;
-    float v = 1.0f * run;  // Block::dot's head: 1.0 for these forms
+    const float head = BF::HEAD ? *(const float *)p.w : 1.0f;  // Block::dot: head * sum
+    float v = head * run;
     const size_t at = (size_t)m * N + r0 + rr;
     if (p.stages & TS_AFTER_ADD) v += p.a0[at];
     if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
@@ -189,46 +166,65 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
 
 using Kern = void (*)(BlockParams);
 
-template <int FORM, bool XF32>
+template <int F, bool XF32>
 Kern pick_m(uint32_t m) {
-    return m == 1 ? block_gemv_kernel<FORM, 1, XF32>
-         : m == 2 ? block_gemv_kernel<FORM, 2, XF32> : block_gemv_kernel<FORM, 4, XF32>;
+    return m == 1 ? block_gemv_kernel<F, 1, XF32>
+         : m == 2 ? block_gemv_kernel<F, 2, XF32> : block_gemv_kernel<F, 4, XF32>;
 }
 
-template <int FORM>
+template <int F>
 Kern pick_x(uint32_t m, bool xf) {
-    return xf ? pick_m<FORM, true>(m) : pick_m<FORM, false>(m);
+    return xf ? pick_m<F, true>(m) : pick_m<F, false>(m);
+}
+
+template <int F>
+constexpr BlockShape shape_of() {
+    using BF = BlockForm<F>;
+    return BlockShape{BF::B, BF::BB, BF::HEAD};
 }
 
 }  // namespace
 
-bool block_form(int32_t dtype) {
-    return dtype == TS_Q8_0 || dtype == TS_MXFP8 || dtype == TS_INT4_G32 || dtype == TS_Q4_0;
+bool block_form(int32_t dtype) { return dtype >= TS_Q8_0 && dtype <= TS_INT4_G128; }
+
+BlockShape block_shape(int32_t dtype) {
+    constexpr BlockShape s[7] = {shape_of<0>(), shape_of<1>(), shape_of<2>(), shape_of<3>(),
+                                 shape_of<4>(), shape_of<5>(), shape_of<6>()};
+    return s[dtype - TS_Q8_0];
 }
 
-size_t block_row_bytes(int32_t dtype, uint32_t k) {
-    const size_t bb = dtype == TS_Q8_0 ? Form<0>::kBytes : dtype == TS_MXFP8 ? Form<1>::kBytes : Form<2>::kBytes;  // q4_0: 18 as int4_g32
-    return (size_t)(k / 32) * bb;
+int block_check(const ts_linear_args *a, const char *rule) {
+    TS_REQUIRE(a && a->x && a->w && a->out, "%s (block form): null pointer", rule);
+    const BlockShape bs = block_shape(a->w_dtype);
+    TS_REQUIRE(a->n >= 1 && a->k >= 128 && a->k % (4 * bs.block) == 0,
+               "%s (block form): k=%u must be a multiple of %u and at least 128", rule, a->k, 4 * bs.block);
+    TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "%s (block form): x dtype %d", rule, a->x_dtype);
+    TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "%s (block form): out dtype %d", rule,
+               a->out_dtype);
+    TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "%s (block form): TS_AFTER_ADD needs a0", rule);
+    TS_REQUIRE(aligned(a->x, 16) && aligned(a->w, 4), "%s (block form): x 16-byte and w 4-byte aligned", rule);
+    return TS_OK;
 }
 
 int block_gemv_launch(const ts_linear_args *a, void *stream) {
-    TS_REQUIRE(a && a->x && a->w && a->out, "lanes (block form): null pointer");
-    TS_REQUIRE(a->m >= 1 && a->m <= 4, "lanes (block form): m=%u outside 1..4 (block forms decode rows only)",
-               a->m);
-    TS_REQUIRE(a->n >= 1 && a->k >= 128 && a->k % 128 == 0, "lanes (block form): k=%u must be a multiple of 128",
-               a->k);
-    TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "lanes (block form): x dtype %d", a->x_dtype);
-    TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "lanes (block form): out dtype %d", a->out_dtype);
+    const int bad = block_check(a, "lanes");
+    if (bad) return bad;
+    TS_REQUIRE(a->m >= 1 && a->m <= 4, "lanes (block form): m=%u outside 1..4 (the decode product)", a->m);
     TS_REQUIRE((a->stages & ~TS_AFTER_ADD) == 0, "lanes (block form): stages %#x (only TS_AFTER_ADD)", a->stages);
-    TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "lanes (block form): TS_AFTER_ADD needs a0");
-    TS_REQUIRE(aligned(a->x, 16) && aligned(a->w, 4), "lanes (block form): x 16-byte and w 4-byte aligned");
     BlockParams p;
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     const bool xf = a->x_dtype == TS_F32;
-    Kern k = a->w_dtype == TS_Q8_0    ? pick_x<0>(a->m, xf)
-           : a->w_dtype == TS_MXFP8   ? pick_x<1>(a->m, xf)
-           : a->w_dtype == TS_INT4_G32 ? pick_x<2>(a->m, xf) : pick_x<3>(a->m, xf);
+    Kern k;
+    switch (a->w_dtype) {
+    case TS_Q8_0: k = pick_x<0>(a->m, xf); break;
+    case TS_MXFP8: k = pick_x<1>(a->m, xf); break;
+    case TS_INT4_G32: k = pick_x<2>(a->m, xf); break;
+    case TS_Q4_0: k = pick_x<3>(a->m, xf); break;
+    case TS_NVFP4: k = pick_x<4>(a->m, xf); break;
+    case TS_MXFP4: k = pick_x<5>(a->m, xf); break;
+    default: k = pick_x<6>(a->m, xf); break;
+    }
     hipLaunchKernelGGL(k, dim3((a->n + kWaves * kRows - 1) / (kWaves * kRows)), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("lanes (block form) launch");
     return TS_OK;

@@ -40,11 +40,17 @@ inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 // The vector-ALU product for m <= 4 rows (gemv.hip); arguments already checked.
 int gemv_launch(const ts_linear_args *a, void *stream);
 
-// Block-form weights (TS_Q8_0, TS_MXFP8, TS_INT4_G32) on the m <= 4 product
-// (blocks.hip): checks its own arguments.
+// Block-form weights (TS_Q8_0 .. TS_INT4_G128): codes a block, bytes a block, head
+// bytes (blocks.hip); the m <= 4 decode product (blocks.hip) and the matrix-unit
+// product for more rows (blockmat.hip), each checking its own arguments.
+struct BlockShape {
+    uint32_t block, bytes, head;
+};
 bool block_form(int32_t dtype);
-size_t block_row_bytes(int32_t dtype, uint32_t k);
+BlockShape block_shape(int32_t dtype);
+int block_check(const ts_linear_args *a, const char *rule);
 int block_gemv_launch(const ts_linear_args *a, void *stream);
+int block_tiled_launch(const ts_linear_args *a, void *stream);
 
 // The 256x256 tiled kernel (tiled_big.hip): TS_OK when launched, 1 when the
 // product is not its shape (bf16 x and w, no SiLU pair, enough tiles), else an error.

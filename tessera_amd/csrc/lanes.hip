@@ -404,7 +404,8 @@ extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
 }
 
 extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
-    if (a && ts::block_form(a->w_dtype)) return ts::block_gemv_launch(a, stream);
+    if (a && ts::block_form(a->w_dtype))
+        return a->m <= 4 ? ts::block_gemv_launch(a, stream) : ts::block_tiled_launch(a, stream);
     int rc = check(a);
     if (rc) return rc;
     if (a->m <= 4) return ts::gemv_launch(a, stream);

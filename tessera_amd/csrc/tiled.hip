@@ -602,6 +602,7 @@ Kern pick_kernel(bool xf, bool w8, bool silu) {
 }  // namespace
 
 extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
+    if (a && ts::block_form(a->w_dtype)) return ts::block_tiled_launch(a, stream);
     TS_REQUIRE(a && a->x && a->w && a->out, "tiled: null pointer");
     TS_REQUIRE(a->m >= 1 && a->n >= 1 && a->k >= 1, "tiled: empty product m=%u n=%u k=%u", a->m, a->n, a->k);
     TS_REQUIRE(a->k % 8 == 0, "tiled: k=%u must be a multiple of 8", a->k);

@@ -55,7 +55,8 @@ def workspace(device) -> Workspace:
     return _ws[key]
 
 
-BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_INT4_G32, "q4_0": abi.TS_Q4_0}
+BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_INT4_G32, "q4_0": abi.TS_Q4_0,
+               "nvfp4": abi.TS_NVFP4, "mxfp4": abi.TS_MXFP4, "int4_g128": abi.TS_INT4_G128}
 
 
 def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6, w_form=None):
@@ -66,16 +67,20 @@ def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e
                                                 _ptr(out))
     a.m, a.n, a.k = m, n, k
     a.x_dtype, a.out_dtype = _DT[x.dtype], _DT[out.dtype]
-    # Block forms: w is the packed bytes [n, k / 32 * block bytes] (uint8).
+    # Block forms: w is the packed tensor (uint8: head, then each row's blocks).
     a.w_dtype = BLOCK_FORMS[w_form] if w_form is not None else _DT[w.dtype]
     a.stages, a.eps = stages, eps
     return a
 
 
 def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, gain=None, a0=None,
-            silu_mul=False, eps=1e-6, w_form=None):
+            silu_mul=False, eps=1e-6, w_form=None, rows=None):
+    """rows: the weight rows of a packed block-form tensor (w is then flat bytes)."""
     m = x.shape[0]
-    n = w.shape[0] // 2 if silu_mul else w.shape[0]
+    wr = rows if w_form is not None else w.shape[0]
+    if wr is None:
+        raise ValueError("a block-form weight tensor needs rows=")
+    n = wr // 2 if silu_mul else wr
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     stages = (abi.TS_AFTER_ADD if a0 is not None else 0) | (abi.TS_AFTER_SILU_MUL if silu_mul else 0) | \

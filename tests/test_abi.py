@@ -110,4 +110,5 @@ def test_dtype_enum_matches_header():
     pairs = dict((k.strip(), int(v)) for k, v in (e.split("=") for e in enum.split(",")))
     assert pairs == {"TS_F32": abi.TS_F32, "TS_BF16": abi.TS_BF16, "TS_E4M3": abi.TS_E4M3, "TS_U32": abi.TS_U32,
                      "TS_Q8_0": abi.TS_Q8_0, "TS_MXFP8": abi.TS_MXFP8, "TS_INT4_G32": abi.TS_INT4_G32,
-                     "TS_Q4_0": abi.TS_Q4_0}
+                     "TS_Q4_0": abi.TS_Q4_0, "TS_NVFP4": abi.TS_NVFP4, "TS_MXFP4": abi.TS_MXFP4,
+                     "TS_INT4_G128": abi.TS_INT4_G128}
