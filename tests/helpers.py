@@ -51,6 +51,14 @@ def product_bound(x, w, *, x_bits=None, parts=1, lane=8):
     return bound
 
 
+def linear_bound(x, w, lane=8):
+    """product_bound for the linear kernels' operands: rows whose values are all bf16
+    enter exactly; other f32 rows as two bf16 parts."""
+    x = np.asarray(x, np.float32)
+    exact = np.array_equal(O.bf16_round(x), x)
+    return product_bound(x, w, x_bits=None if exact else 16, parts=1 if exact else 2, lane=lane)
+
+
 def assert_within(got, want, bound):
     """|got - want| <= bound per element, and the bound says something: below a tenth
     of the largest output (tiled_test.rs:104-114)."""
