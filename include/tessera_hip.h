@@ -53,6 +53,9 @@ enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 =
 #define TS_AFTER_ADD 1u       /* out = sum + a0[m, n] (the residual add; a0 may alias out) */
 #define TS_AFTER_SILU_MUL 2u  /* w holds 2n rows, gate rows then up rows; out = silu(g) * u */
 #define TS_BEFORE_RMS_NORM 4u /* x rows pass through RmsNorm with `gain` before the product */
+#define TS_AFTER_ARGMAX 8u    /* m <= 4, f32 out, no SiLU pair: out as usual, and each row's
+                                 greedy pick folded into workspace key[m] (uint64; zero before
+                                 the launch): tessera_hip_argmax_keys reads and clears them */
 
 /* Version of this ABI; bumped on any struct layout change. */
 #define TS_ABI_VERSION 2
@@ -292,6 +295,13 @@ int tessera_hip_mix(const float *x, const float *weights, float *out, uint32_t o
 int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, uint32_t width,
                        void *workspace, size_t workspace_bytes, void *stream);
 size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width);
+
+/* ids[r] from the keys a product with TS_AFTER_ARGMAX folded (the same pick as
+ * tessera_hip_argmax over its output row: first index of the largest entry, NaN and
+ * -inf skipped, `width` when none), then keys[r] = 0 for the next product.
+ * No counterpart in the reference: argmax fused into the lm_head product, so the
+ * logits are not read back (engine/rules/kernels/src/argmax.rs:74-129 reads them). */
+int tessera_hip_argmax_keys(uint64_t *keys, uint32_t *ids, uint32_t rows, uint32_t width, void *stream);
 
 /* ids[r, 0..k): the row's k largest finite entries, best first, ties to the
  * lower index, NaN/-inf skipped, spare slots = width. x f32 [rows, width],

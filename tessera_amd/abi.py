@@ -29,6 +29,7 @@ TS_NVFP4, TS_MXFP4, TS_INT4_G128 = 8, 9, 10
 TS_AFTER_ADD = 1
 TS_AFTER_SILU_MUL = 2
 TS_BEFORE_RMS_NORM = 4
+TS_AFTER_ARGMAX = 8
 
 U32_MAX = 0xFFFFFFFF
 
@@ -102,6 +103,7 @@ SIGNATURES = {
     "tessera_hip_gather": (C.c_int, [_P, _P, _P, _U, _U, _U, _U, _P]),
     "tessera_hip_argmax": (C.c_int, [_P, _P, _U, _U, _P, C.c_size_t, _P]),
     "tessera_hip_argmax_workspace": (C.c_size_t, [_U, _U]),
+    "tessera_hip_argmax_keys": (C.c_int, [_P, _P, _U, _U, _P]),
     "tessera_hip_top_k": (C.c_int, [_P, _P, _U, _U, _U, _P]),
 }
 

@@ -121,6 +121,15 @@ TS_DEV void e4m3x4_to_f32(uint32_t w, float *f) {
     f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
 }
 
+// The argmax key of entry n with value v, ordered as the pick (argmax_spans):
+// larger values first, then lower indices; 0 (never the max) for NaN and -inf.
+TS_DEV uint64_t argmax_key(float v, uint32_t n) {
+    if (!(v > -__builtin_inff())) return 0;  // NaN or -inf
+    const uint32_t f = __float_as_uint(v);
+    const uint32_t ord = (f & 0x80000000u) ? ~f : (f | 0x80000000u);
+    return ((uint64_t)ord << 32) | (uint32_t)~n;
+}
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions (DPP/permute via the compiler's __shfl_xor).
 // ---------------------------------------------------------------------------

@@ -38,6 +38,7 @@ struct GemvParams {
     uint32_t stages;
     float eps;
     int out_bf16;
+    void *keys;  // TS_AFTER_ARGMAX: [m] uint64
     uint32_t waves;  // waves per group splitting k
 };
 
@@ -247,9 +248,9 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
         }
     }
     // Lane t of wave 0 finishes output (t / M, t % M).
-    if (wave != 0 || lane >= outs * M) return;
+    if (wave != 0) return;
     const uint32_t o = lane / M, m = lane % M;
-    if (m >= Mr || o0 + o >= N) return;
+    const bool live = lane < outs * M && m < Mr && o0 + o < N;
     float g = 0.0f, u = 0.0f, sq = 0.0f;
 #pragma unroll
     for (int r = 0; r < R; r++)
@@ -273,8 +274,24 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
     }
     float v = silu ? g / (1.0f + expf(-g)) * u : g;
     if (p.stages & TS_AFTER_ADD) v += pre_a0;
-    if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
-    else ((float *)p.out)[(size_t)m * N + n] = v;
+    if (live) {
+        if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
+        else ((float *)p.out)[(size_t)m * N + n] = v;
+    }
+    if (p.stages & TS_AFTER_ARGMAX) {
+        // The group's best entry per row (lanes m, m + M, ... share row m), folded into
+        // keys[m] only when it beats what is there: after the first few groups almost
+        // none does, so few atomics reach the one address.
+        uint64_t key = live ? argmax_key(v, n) : 0;
+#pragma unroll
+        for (int off = M; off < 64; off *= 2) {
+            const uint64_t other = __shfl_xor(key, off);
+            key = other > key ? other : key;
+        }
+        uint64_t *keys = (uint64_t *)p.keys;
+        if (lane < M && m < Mr && key > __hip_atomic_load(keys + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+            __hip_atomic_fetch_max(keys + m, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 using Kern = void (*)(GemvParams);
@@ -337,7 +354,7 @@ int gemv_launch(const ts_linear_args *a, void *stream) {
     GemvParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.gain = a->gain; p.a0 = a->a0;
     p.out = a->out; p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.eps = a->eps;
-    p.out_bf16 = a->out_dtype == TS_BF16; p.waves = w;
+    p.out_bf16 = a->out_dtype == TS_BF16; p.waves = w; p.keys = a->workspace;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
     Kern k = xf ? (w8 ? pick_m<true, true>(a->m, r) : pick_m<true, false>(a->m, r))
                 : (w8 ? pick_m<false, true>(a->m, r) : pick_m<false, false>(a->m, r));

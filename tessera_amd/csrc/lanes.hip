@@ -387,15 +387,22 @@ int check(const ts_linear_args *a) {
     TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "lanes: TS_AFTER_ADD needs a0");
     TS_REQUIRE(!(a->stages & TS_BEFORE_RMS_NORM) || (a->gain && a->x_dtype == TS_F32 && a->m <= 16),
                "lanes: TS_BEFORE_RMS_NORM needs gain, f32 x and m <= 16");
-    TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL | TS_BEFORE_RMS_NORM)) == 0,
+    TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL | TS_BEFORE_RMS_NORM | TS_AFTER_ARGMAX)) == 0,
                "lanes: unknown stage bits %#x", a->stages);
     TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "lanes: x and w must be 16-byte aligned");
+    if (a->stages & TS_AFTER_ARGMAX) {
+        TS_REQUIRE(a->m <= 4 && a->out_dtype == TS_F32 && !(a->stages & TS_AFTER_SILU_MUL),
+                   "lanes: TS_AFTER_ARGMAX needs m <= 4, f32 out and no SiLU pair");
+        if (!a->workspace || a->workspace_bytes < (size_t)a->m * 8 || !ts::aligned(a->workspace, 8))
+            return ts::fail(TS_ERR_WORKSPACE, "lanes: TS_AFTER_ARGMAX needs %u 8-byte-aligned keys", a->m);
+    }
     return TS_OK;
 }
 
 }  // namespace
 
 extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
+    if (a && (a->stages & TS_AFTER_ARGMAX)) return (size_t)a->m * 8;  // the keys
     if (!a || a->m <= 4 || a->m > 64 || ts::block_form(a->w_dtype)) return 0;
     const Plan pl = plan(a);
     if (pl.splits <= 1) return 0;

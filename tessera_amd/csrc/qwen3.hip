@@ -11,8 +11,8 @@
 //     lanes(attn, o, after +x)                      -> x
 //     lanes(x, gate_up, before RmsNorm(ln2), silu*) -> h          [1, F]
 //     lanes(h, down, after +x)                      -> x
-//   lanes(x, embed, before RmsNorm(norm))           -> logits     [1, V]
-//   argmax(logits) -> tok; advance(pos)
+//   lanes(x, embed, before RmsNorm(norm), argmax)   -> logits     [1, V], key
+//   advance: tok from key; pos + 1
 // Position and token live in device memory, so one captured graph serves
 // every step (engine/plan/run/src/device.rs:227-245 captures per size binding).
 #include <string.h>
@@ -55,17 +55,28 @@ __global__ void init_gain_kernel(float *g, uint64_t n, uint64_t seed, uint64_t t
         g[i] = bf16_round(1.0f + std * seeded_normal(seed, tensor, i));
 }
 
-// After a decode step: record the new token and move to the next position.
-__global__ void advance_kernel(const uint32_t *tok, uint32_t *pos, uint32_t *hist) {
+// The greedy token from the key the lm_head product folded (TS_AFTER_ARGMAX), and the
+// key cleared for the next product.
+TS_DEV uint32_t take_token(uint64_t *key, uint32_t *tok, uint32_t vocab) {
+    const uint64_t k = key[0];
+    const uint32_t t = k ? ~(uint32_t)k : vocab;
+    key[0] = 0;
+    tok[0] = t;
+    return t;
+}
+
+// After a decode step: the new token, recorded, and the next position.
+__global__ void advance_kernel(uint64_t *key, uint32_t *tok, uint32_t *pos, uint32_t *hist, uint32_t vocab) {
     const uint32_t p = pos[0] + 1;
-    hist[p] = tok[0];
+    hist[p] = take_token(key, tok, vocab);
     pos[0] = p;
 }
 
 // After a prefill of `count` rows: the first new token sits at position count.
-__global__ void start_kernel(const uint32_t *tok, uint32_t *pos, uint32_t *hist, uint32_t count) {
+__global__ void start_kernel(uint64_t *key, uint32_t *tok, uint32_t *pos, uint32_t *hist, uint32_t count,
+                             uint32_t vocab) {
     pos[0] = count;
-    hist[count] = tok[0];
+    hist[count] = take_token(key, tok, vocab);
 }
 
 struct Layer {
@@ -86,6 +97,7 @@ struct ts_qwen3 {
     // activations
     float *x, *xn, *qkv, *q, *attn, *h, *logits, *rope;
     uint32_t *d_tok, *d_pos, *d_slot, *d_hist, *d_prompt, *d_prompt_pos, *d_prompt_slot, *d_table;
+    uint64_t *d_key = nullptr;  // the lm_head product's folded argmax (zero between steps)
     void *ws = nullptr;
     size_t ws_bytes = 0;
     void **d_buffers = nullptr;  // the K and V kept-row buffers of every layer (page copies)
@@ -214,14 +226,16 @@ int run_layers(ts_qwen3 *m, uint32_t rows, const uint32_t *slots, const uint32_t
     return TS_OK;
 }
 
-// Logits of one row (`row` of x) and the greedy token.
+// Logits of one row (`row` of x), the greedy pick folded into d_key by the same
+// product (start_kernel / advance_kernel turn it into the token).
 int head(ts_qwen3 *m, uint32_t row) {
     const ts_qwen3_config &c = m->c;
     ts_linear_args a = lin(m->x + (size_t)row * c.hidden, m->embed, m->logits, 1, c.vocab, c.hidden, m);
-    a.stages = TS_BEFORE_RMS_NORM;
+    a.stages = TS_BEFORE_RMS_NORM | TS_AFTER_ARGMAX;
     a.gain = m->norm;
-    TRY(tessera_hip_linear(&a, m->stream));
-    return tessera_hip_argmax(m->logits, m->d_tok, 1, c.vocab, m->ws, m->ws_bytes, m->stream);
+    a.workspace = m->d_key;
+    a.workspace_bytes = 8;
+    return tessera_hip_linear(&a, m->stream);
 }
 
 int decode_step(ts_qwen3 *m) {
@@ -229,7 +243,8 @@ int decode_step(ts_qwen3 *m) {
     TRY(tessera_hip_gather(m->embed, m->d_tok, m->x, 1, c.vocab, c.hidden, 0, m->stream));
     TRY(run_layers(m, 1, m->d_slot, m->d_pos, c.max_context - 1));
     TRY(head(m, 0));
-    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, m->stream, m->d_tok, m->d_pos, m->d_hist);
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, m->stream, m->d_key, m->d_tok, m->d_pos, m->d_hist,
+                       c.vocab);
     TS_CHECK_LAUNCH("advance");
     return TS_OK;
 }
@@ -350,8 +365,11 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
         (rc = m->alloc(&m->d_hist, (size_t)c.max_context + 1)) || (rc = m->alloc(&m->d_prompt, R)) ||
         (rc = m->alloc(&m->d_prompt_pos, R)) || (rc = m->alloc(&m->d_prompt_slot, R)) ||
         (rc = m->alloc(&m->d_table, m->kept_pages)) || (rc = m->alloc(&m->rope, (size_t)c.max_context * D)) ||
-        (rc = m->alloc(&m->d_buffers, 2 * (size_t)c.layers)) || (rc = m->alloc(&m->d_copy, 1)))
+        (rc = m->alloc(&m->d_buffers, 2 * (size_t)c.layers)) || (rc = m->alloc(&m->d_copy, 1)) ||
+        (rc = m->alloc(&m->d_key, 1)))
         return fail(rc);
+    e = hipMemsetAsync(m->d_key, 0, 8, m->stream);
+    if (e != hipSuccess) return fail(ts::hip_status(e, "hipMemsetAsync"));
     {
         std::vector<void *> bufs;
         for (const Layer &L : m->layers) { bufs.push_back(L.k_cache); bufs.push_back(L.v_cache); }
@@ -504,7 +522,8 @@ extern "C" int tessera_qwen3_prefill(ts_qwen3 *m, const uint32_t *tokens, uint32
     TRY(tessera_hip_gather(m->embed, m->d_prompt, m->x, count, c.vocab, c.hidden, 0, m->stream));
     TRY(run_layers(m, count, m->d_prompt_slot, m->d_prompt_pos, count - 1));
     TRY(head(m, count - 1));
-    hipLaunchKernelGGL(start_kernel, dim3(1), dim3(1), 0, m->stream, m->d_tok, m->d_pos, m->d_hist, count);
+    hipLaunchKernelGGL(start_kernel, dim3(1), dim3(1), 0, m->stream, m->d_key, m->d_tok, m->d_pos, m->d_hist, count,
+                       c.vocab);
     TS_CHECK_LAUNCH("start");
     e = hipMemcpyAsync(next, m->d_tok, 4, hipMemcpyDeviceToHost, m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);

@@ -304,6 +304,23 @@ extern "C" int tessera_hip_gather(const void *table, const uint32_t *ids, float 
     return TS_OK;
 }
 
+__global__ void argmax_keys_kernel(uint64_t *keys, uint32_t *ids, uint32_t rows, uint32_t width) {
+    const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const uint64_t key = keys[r];
+    ids[r] = key ? ~(uint32_t)key : width;
+    keys[r] = 0;
+}
+
+extern "C" int tessera_hip_argmax_keys(uint64_t *keys, uint32_t *ids, uint32_t rows, uint32_t width, void *stream) {
+    TS_REQUIRE(keys && ids, "argmax_keys: null pointer");
+    if (rows == 0) return TS_OK;
+    hipLaunchKernelGGL(argmax_keys_kernel, dim3((rows + 255) / 256), dim3(256), 0, (hipStream_t)stream, keys, ids,
+                       rows, width);
+    TS_CHECK_LAUNCH("argmax_keys launch");
+    return TS_OK;
+}
+
 extern "C" size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width) {
     const size_t spans = (width + kSpan - 1) / kSpan;
     return (size_t)rows * spans * (sizeof(float) + sizeof(uint32_t));

@@ -290,6 +290,22 @@ def argmax(x, ids=None):
     return ids
 
 
+def linear_argmax(x, w, *, gain=None, eps=1e-6, keys=None):
+    """The few-row product with the greedy pick folded in (TS_AFTER_ARGMAX): (logits,
+    ids). `keys` (int64 [m], zero) may be passed to reuse; it is zero again after."""
+    m, n = x.shape[0], w.shape[0]
+    out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    if keys is None:
+        keys = torch.zeros(m, dtype=torch.int64, device=x.device)
+    stages = abi.TS_AFTER_ARGMAX | (abi.TS_BEFORE_RMS_NORM if gain is not None else 0)
+    a = linear_args(x, w, out, gain=gain, stages=stages, eps=eps)
+    a.workspace, a.workspace_bytes = _ptr(keys), keys.numel() * 8
+    abi.call("tessera_hip_lanes", C.byref(a), _stream())
+    ids = torch.empty(m, dtype=torch.int32, device=x.device)
+    abi.call("tessera_hip_argmax_keys", _ptr(keys), _ptr(ids), m, n, _stream())
+    return out, ids
+
+
 def top_k(x, k, ids=None):
     rows, width = x.shape
     if ids is None:

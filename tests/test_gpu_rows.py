@@ -132,3 +132,34 @@ def test_rope_table_matches_angles():
         for j in (0, 1, 31, 63):
             ang = O.angle(pos, j, 128, 1e6)
             assert abs(t[pos, j, 0] - math.cos(ang)) < 2e-6 and abs(t[pos, j, 1] - math.sin(ang)) < 2e-6
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_argmax_fused_into_the_product(m):
+    """TS_AFTER_ARGMAX: the pick folded into the lm_head product equals argmax over the
+    logits the same launch wrote (first index of the max; NaN and -inf skipped), with
+    two identical weight rows (a tie), a NaN row and a -inf row; the keys are zero again
+    after, so a second call reuses them."""
+    n, k = 151936, 1024
+    r = rng(40 + m)
+    wbits, _ = bf16_bits_normal(r, (n, k), 0.02)
+    wbits[90000] = wbits[1000] = O.bf16_narrow(np.full(k, 0.5, np.float32))  # large and equal
+    wbits[5] = O.bf16_narrow(np.full(k, np.nan, np.float32))
+    wbits[6] = O.bf16_narrow(np.full(k, -np.inf, np.float32))
+    x = np.abs(r.standard_normal((m, k))).astype(np.float32)
+    g = (1.0 + 0.1 * r.standard_normal(k)).astype(np.float32)
+    keys = torch.zeros(m, dtype=torch.int64, device="cuda")
+    for _ in range(2):
+        logits, ids = R().linear_argmax(to_dev(x, torch), to_dev(wbits, torch), gain=to_dev(g, torch), keys=keys)
+        lg = from_dev(logits)
+        assert np.isnan(lg[:, 5]).all() and np.isneginf(lg[:, 6]).all()
+        assert from_dev(ids).tolist() == O.top_k(lg, 1).reshape(-1).astype(np.int64).tolist() == [1000] * m
+        assert from_dev(keys).tolist() == [0] * m
+
+
+def test_argmax_fused_nothing_finite():
+    k = 256
+    w = O.bf16_narrow(np.full((300, k), -np.inf, np.float32))
+    x = np.ones((1, k), np.float32)
+    logits, ids = R().linear_argmax(to_dev(x, torch), to_dev(w, torch))
+    assert np.isneginf(from_dev(logits)).all() and from_dev(ids).tolist() == [300]
