@@ -321,14 +321,16 @@ def c5(torch):
             "frac": round(roof / t, 4)}
 
 
-def cpu_baseline(model, prompt, steps):
+def cpu_baseline(model, prompt, steps, threads=None):
     """The oracle decoding `steps` tokens after the same prompt, kept rows copied from
-    the device after its prefill; all host cores (up to 16) via OpenMP."""
+    the device after its prefill; `threads` host cores (default: all, up to 16) via
+    OpenMP over output columns, or 1 (the reference interpreter's single-threaded
+    order, engine/ir/interp/src/round.rs:8-34)."""
     import numpy as np
 
     import oracle as O
     from oracle.qwen3 import Qwen3 as OracleQwen3, from_runner
-    threads = min(16, os.cpu_count() or 1)
+    threads = threads or min(16, os.cpu_count() or 1)
     O.set_threads(threads)
     ref = OracleQwen3(from_runner(model))
     c = model.config
@@ -346,9 +348,10 @@ def cpu_baseline(model, prompt, steps):
         logits = ref.forward([tok], [PROMPT + i])
         tok = int(np.argmax(logits))
     dt = time.perf_counter() - t0
+    how = f"OpenMP over output columns, {threads} threads" if threads > 1 else "one thread, reference order"
     return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "sample": f"{steps} greedy decode steps at context {PROMPT}..{PROMPT + steps} "
-                      f"(oracle restatement of tessera-interp, OpenMP over output columns, {threads} threads)"}
+                      f"(oracle restatement of tessera-interp, {how})"}
 
 
 def main():
@@ -405,6 +408,7 @@ def main():
     cpu = None
     if not a.no_cpu and a.cpu_steps > 0:
         cpu = cpu_baseline(m, prompt, a.cpu_steps)
+        cpu["single_thread"] = cpu_baseline(m, prompt, 1, threads=1)
     m.close()
     if not a.no_rows:
         torch.cuda.empty_cache()
