@@ -57,8 +57,11 @@ constexpr int kTilesQkv = 4, kTilesO = 2, kTilesGu = 4, kTilesDn = 2;
 enum Role : uint32_t { kQkv = 0, kO = 1, kGu = 2, kDn = 3, kAtt = 4 };
 
 // LDS layout (bytes).
-constexpr uint32_t kXsOff = 0;                            // staged inputs, 3 bf16 parts [2][3][kMaxF]
-constexpr uint32_t kResOff = kXsOff + 2 * 3 * kMaxF * 2;  // residual rows [2][64]
+// A staged part is kXsCol bf16 long: 16 bytes past kMaxF, so the three parts one
+// fragment read touches start on different banks (kMaxF * 2 bytes is a multiple of 256).
+constexpr uint32_t kXsCol = kMaxF + 8;
+constexpr uint32_t kXsOff = 0;                             // staged inputs, 3 bf16 parts [2][3][kXsCol]
+constexpr uint32_t kResOff = kXsOff + 2 * 3 * kXsCol * 2;  // residual rows [2][64]
 constexpr uint32_t kSsqOff = kResOff + 2 * 64 * 4;        // sums of squares [2][kW]
 constexpr uint32_t kPartOff = kSsqOff + 2 * kW * 4;       // per-wave row partials [2][kW][64]
 constexpr uint32_t kLmPartOff = kPartOff + 2 * kW * 64 * 4;  // lm_head row partials [kW][kMaxLm]
@@ -126,7 +129,7 @@ struct Ctx {
     uint32_t *tbl;
     uint32_t tid, wave, lane, g;
     uint32_t ph;  // staging parity
-    TS_DEV uint16_t *xs() const { return (uint16_t *)(lds + kXsOff) + (ph & 1) * 3 * kMaxF; }
+    TS_DEV uint16_t *xs() const { return (uint16_t *)(lds + kXsOff) + (ph & 1) * 3 * kXsCol; }
     TS_DEV float *res() const { return (float *)(lds + kResOff) + (ph & 1) * 64; }
     TS_DEV float *ssq() const { return (float *)(lds + kSsqOff) + (ph & 1) * kW; }
     TS_DEV float *part() const { return (float *)(lds + kPartOff) + (ph & 1) * kW * 64; }
@@ -238,8 +241,8 @@ TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX]
             const float r1 = x - bf16_float(hi);
             const uint16_t mid = bf16_bits(r1);
             xs[i] = hi;
-            xs[kMaxF + i] = mid;
-            xs[2 * kMaxF + i] = bf16_bits(r1 - bf16_float(mid));
+            xs[kXsCol + i] = mid;
+            xs[2 * kXsCol + i] = bf16_bits(r1 - bf16_float(mid));
             ss += v[k] * v[k];
         }
     }
@@ -283,10 +286,13 @@ __host__ __device__ inline uint32_t lm_tiles(uint32_t V, uint32_t NG) { return (
 
 // B fragment of k-step ks from the staged input: column 0 the high parts of k values
 // ks * 32 + 8 (l / 16) .. +8, column 1 the middle, column 2 the low, the rest zero.
+// Branch-free: every lane reads (the other columns a part that exists) and zeroes by
+// select, so a role's reads of all its k-steps issue back to back before the MFMAs.
 TS_DEV u32x4 x_frag(const Ctx &c, const uint16_t *xs, uint32_t ks, uint32_t K) {
     const uint32_t col = c.lane & 15, k0 = ks * 32 + (c.lane >> 4) * 8;
-    if (col >= 3 || k0 >= K) return u32x4{0, 0, 0, 0};
-    return *(const u32x4 *)&xs[col * kMaxF + k0];
+    const bool live = col < 3 && k0 < K;
+    const u32x4 v = *(const u32x4 *)&xs[(col < 3 ? col : 0) * kXsCol + (k0 < K ? k0 : 0)];
+    return live ? v : u32x4{0, 0, 0, 0};
 }
 
 // The tile's row sums (columns 0 + 1 + 2) into part[t * 16 + row] from lanes 0, 16,
@@ -524,11 +530,27 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
                 f32x4 acc[TILES];
 #pragma unroll
                 for (int t2 = 0; t2 < TILES; t2++) acc[t2] = f32x4{0, 0, 0, 0};
+                // The input fragments in chunks of CH k-steps, the next chunk's reads
+                // issued before this chunk's MFMAs (the order pinned: the LDS latency
+                // then hides under matrix work instead of preceding every step).
+                constexpr int CH = KS < 4 ? KS : 4;
+                u32x4 xb[2][CH];
 #pragma unroll
-                for (int j = 0; j < KS; j++) {
-                    const u32x4 xb = x_frag(c, xs, c.wave * KS + j, K);
+                for (int j = 0; j < CH; j++) xb[0][j] = x_frag(c, xs, c.wave * KS + j, K);
 #pragma unroll
-                    for (int t2 = 0; t2 < TILES; t2++) acc[t2] = mfma16(as_bf16x8(w[t2][j]), as_bf16x8(xb), acc[t2]);
+                for (int j0 = 0; j0 < KS; j0 += CH) {
+                    const int cur = (j0 / CH) & 1;
+                    if (j0 + CH < KS) {
+#pragma unroll
+                        for (int j = 0; j < CH; j++) xb[cur ^ 1][j] = x_frag(c, xs, c.wave * KS + j0 + CH + j, K);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int j = 0; j < CH; j++)
+#pragma unroll
+                        for (int t2 = 0; t2 < TILES; t2++)
+                            acc[t2] = mfma16(as_bf16x8(w[t2][j0 + j]), as_bf16x8(xb[cur][j]), acc[t2]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
 #pragma unroll
                 for (int t2 = 0; t2 < TILES; t2++) tile_out(c, acc[t2], part + c.wave * 64, t2);
@@ -664,6 +686,9 @@ TS_DEV void att_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t h
                 }
             }
             bar();
+#ifdef TS_FINE
+            mark(p, c, t, l, 2);
+#endif
             float q[8];
             {
                 const float4 q0 = *(const float4 *)&qs[8 * part], q1 = *(const float4 *)&qs[8 * part + 4];
@@ -728,6 +753,9 @@ TS_DEV void att_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t h
 #pragma unroll
                 for (int e = 0; e < 8; e++) o[e] = o[e] * alpha + acc[e];
             }
+#ifdef TS_FINE
+            mark(p, c, t, l, 3);
+#endif
             // Sum the four key rows; lanes of row 0 hold the wave's partial sums.
 #pragma unroll
             for (int e = 0; e < 8; e++) o[e] = rows4_sum(o[e]);
@@ -741,6 +769,9 @@ TS_DEV void att_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t h
                 pl[wave] = ls;
             }
             bar();
+#ifdef TS_FINE
+            mark(p, c, t, l, 4);
+#endif
             if (c.tid < 128) {
                 const uint32_t d = c.tid;
                 float M = -INFINITY;
