@@ -70,4 +70,23 @@ TS_DEV float block_code(const uint8_t *codes, int j) {
     return BF::CODE == kCodeNibble ? (float)c - 8.0f : e2m1_value(c);
 }
 
+// Codes q P .. q P + P - 1 of the block into wv (exact, before the scale). e2m1 pairs
+// convert two at a time on gfx950's fp4 conversion (scale 1: exact).
+template <int F, int P>
+TS_DEV void block_codes(const uint8_t *codes, int q, float *wv) {
+    using BF = BlockForm<F>;
+    if (BF::CODE == kCodeE2M1 && !BF::HALVES) {
+        typedef float f32x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+        for (int b = 0; b < P / 2; b++) {
+            const f32x2_t v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4((uint32_t)codes[(q * P) / 2 + b], 1.0f, 0);
+            wv[2 * b] = v.x;
+            wv[2 * b + 1] = v.y;
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < P; j++) wv[j] = block_code<F>(codes, q * P + j);
+}
+
 }  // namespace ts

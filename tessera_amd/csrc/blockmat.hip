@@ -155,11 +155,12 @@ __global__ __launch_bounds__(kThreads) void block_tiled_kernel(MatParams p) {
             if (!FOLD) scales[br][bi] = sc;
 #pragma unroll
             for (int g = 0; g < B / 8; g++) {
+                float cv[8];
+                block_codes<F, 8>(blk + BF::SB, g, cv);
                 uint32_t pk[4];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    float c0 = block_code<F>(blk + BF::SB, 8 * g + 2 * e);
-                    float c1 = block_code<F>(blk + BF::SB, 8 * g + 2 * e + 1);
+                    float c0 = cv[2 * e], c1 = cv[2 * e + 1];
                     if (FOLD) {
                         c0 *= sc;
                         c1 *= sc;

@@ -8,8 +8,8 @@
 //
 // gfx950 design. One wave per 4 weight rows. Blocks are 9 to 66 bytes, not 16-byte
 // aligned: the wave streams its rows' bytes with coalesced 4-byte loads (all four rows
-// in flight together) into its own LDS slices, one block per lane (64 blocks a slice;
-// 16 of the 128-code blocks), and lane l then decodes block l of each row. Each lane
+// in flight together) into its own LDS slices, one block per lane (64 blocks a
+// slice), and lane l then decodes block l of each row. Each lane
 // forms its block's part in the reference's order (x_j times the decoded code, summed
 // from 0.0 in j order, no contraction), times the block scale; lane (row, m) then adds
 // the contributions of activation row m in block order, and the head (nvfp4) scales
@@ -34,9 +34,10 @@ struct BlockParams {
     int out_bf16;
 };
 
-// Blocks per LDS slice: one per lane (16 for 128-code blocks, keeping the slice small).
+// Blocks per LDS slice: one per lane (a 128-code block's part is one ordered sum, so
+// it cannot be split over lanes; its slices take 66 KiB of LDS for the four waves).
 template <int F>
-constexpr int chunk_blocks() { return BlockForm<F>::B == 128 ? 16 : 64; }
+constexpr int chunk_blocks() { return 64; }
 
 // Waits for this wave's LDS traffic so the other lanes' writes are visible.
 TS_DEV void wave_lds_sync() {
@@ -119,15 +120,17 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
 #pragma unroll
                 for (int rr = 0; rr < kRows; rr++) part[rr] = 0.0f;
                 // Block::dot's part: x_j times code j, summed from 0.0 in j order.
-#pragma unroll 1
+#pragma unroll
                 for (int q = 0; q < B / P; q++) {
                     float xv[P];
                     load_x<P, XF32>(p.x, (size_t)m * K + k0 + q * P, xv);
 #pragma unroll
                     for (int rr = 0; rr < kRows; rr++) {
                         const uint8_t *codes = (const uint8_t *)stage[wave][rr] + lane * BB + SB;
+                        float wv[P];
+                        block_codes<F, P>(codes, q, wv);
 #pragma unroll
-                        for (int j = 0; j < P; j++) part[rr] = part[rr] + xv[j] * block_code<F>(codes, q * P + j);
+                        for (int j = 0; j < P; j++) part[rr] = part[rr] + xv[j] * wv[j];
                     }
                 }
 #pragma unroll
