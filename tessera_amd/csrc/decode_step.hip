@@ -16,12 +16,12 @@
 // among 32 ~1.3 us. So each group (one per CU, resident for the whole call) has one
 // role for the whole launch:
 //  * qkv, o, gate/up or down: the group owns fixed rows of that matrix in every
-//    layer and keeps them in registers (<= 72 VGPRs a lane). Right after a layer's
+//    layer and keeps them in registers (<= 96 VGPRs a lane). Right after a layer's
 //    products it issues the loads of the next layer's rows into the same registers,
 //    so they land during the ~10 us until that layer comes round: no weight latency
 //    on the chain, and each hand-off runs between two role sets of 32..96 groups;
-//  * attention: one group per kv head runs both q heads of its pair (the new k/v
-//    row is appended and later read by the same group: no cross-CU ordering);
+//  * attention: one group per q head (both heads of a kv head append the same new k/v
+//    row, bit for bit, and each reads back only rows it wrote: no cross-CU ordering);
 //  * every group then streams its rows of the tied lm_head; every group publishes
 //    its (max, index), and the groups that need the token reduce all of them.
 // Hand-offs are "tagged" words in HBM: each value is one 8-byte store of (f32 value,
