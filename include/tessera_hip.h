@@ -58,7 +58,7 @@ enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 =
                                  the launch): tessera_hip_argmax_keys reads and clears them */
 
 /* Version of this ABI; bumped on any struct layout change. */
-#define TS_ABI_VERSION 2
+#define TS_ABI_VERSION 3
 
 /* Checks that the current device is gfx950 and records its properties.
  * Replaces: the platform probe of engine/gpu/gpukit/src/rocm/context.rs:60-106
@@ -218,9 +218,15 @@ size_t tessera_hip_attend_rows_noalloc_limit(void);
  * share a slot (the decode shape: one new row per slot).
  * Replaces: the q_norm/k_norm RmsNorm + rope + Append + attend_rows chain of
  * engine/models/src/shared.rs:109-145 and engine/ir/interp/src/run.rs:122-198. */
-int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
-                            const float *k_gain, const float *rope_table, uint32_t rope_rows, float eps,
-                            void *stream);
+typedef struct {
+    ts_rows_args rows;          /* as for attend_rows; rows.q is ignored */
+    const float *qkv;           /* [rows, (heads + 2 kv_heads) * width] f32 */
+    const float *q_gain, *k_gain; /* [width] f32 */
+    const float *rope_table;    /* tessera_hip_rope_table's output */
+    uint32_t rope_rows;         /* positions the table holds (> rows.max_position) */
+    float eps;
+} ts_step_args;
+int tessera_hip_attend_step(const ts_step_args *a, void *stream);
 
 /* Prefill: 128-row query blocks on the matrix unit, keys streamed page by page
  * with online softmax. Rows may be packed ragged, back to back: a block whose rows
@@ -231,25 +237,42 @@ int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float
 int tessera_hip_flash_rows(const ts_rows_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------
- * Row stages and indices.
+ * Row stages and indices. Each takes one argument struct, fields in the reference
+ * Launch order (reads, outputs, then counts and scalars), and the stream.
  * ------------------------------------------------------------------------- */
 
 /* out = x * rsqrt(mean(x^2) + eps) * gain, per row of `width`; x/out f32.
  * Replaces: "rms_norm" / "lane_norm" (engine/rules/kernels/src/rms_norm.rs:9-69,
  * lane_norm.rs:10-96). out may alias x. */
-int tessera_hip_rms_norm(const float *x, const float *gain, float *out, uint32_t rows,
-                         uint32_t width, float eps, void *stream);
+typedef struct {
+    const float *x, *gain;  /* reads: [rows, width], [width] */
+    float *out;             /* [rows, width] */
+    uint32_t rows, width;
+    float eps;
+} ts_norm_args;
+int tessera_hip_rms_norm(const ts_norm_args *a, void *stream);
 
 /* Rotates (j, j + width/2) pairs (Halves) or (2j, 2j+1) (Adjacent) of each
  * [rows, heads, width] row in place by angle pos * theta^(-2j/width).
  * Replaces: "angles" + "rope" (engine/rules/kernels/src/rope.rs:10-125). */
-int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t rows, uint32_t heads,
-                     uint32_t width, float theta, int32_t halves, void *stream);
+typedef struct {
+    float *x;                   /* [rows, heads, width], rotated in place */
+    const uint32_t *positions;  /* [rows] */
+    uint32_t rows, heads, width;
+    float theta;
+    int32_t halves;             /* 1: Halves pairs, 0: Adjacent */
+} ts_rope_args;
+int tessera_hip_rope(const ts_rope_args *a, void *stream);
 
 /* The angle table: table[(pos * width/2 + j) * 2 + {0, 1}] = (cos, sin) of
  * pos * theta^(-2j/width) for pos < positions, j < width/2.
  * Replaces: the "angles" stage (engine/rules/kernels/src/rope.rs:10-58). */
-int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t width, float theta, void *stream);
+typedef struct {
+    float *table;  /* [positions][width / 2][2] */
+    uint32_t positions, width;
+    float theta;
+} ts_angles_args;
+int tessera_hip_rope_table(const ts_angles_args *a, void *stream);
 
 /* The step between the q/k/v product and attention for a Qwen3 layer: per head
  * RmsNorm (q_gain / k_gain, eps) then Halves RoPE on q and k, then the new k
@@ -258,57 +281,93 @@ int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t width, flo
  * q_out: [rows, heads, width] f32.
  * Replaces: the q_norm/k_norm RmsNorm + rope + Append chain
  * (engine/models/src/shared.rs:109-145, engine/ir/interp/src/run.rs:122-198). */
-int tessera_hip_qk_norm_rope_append(const float *qkv, const float *q_gain, const float *k_gain,
-                                    float *q_out, void *k_cache, void *v_cache,
-                                    const uint32_t *slots, const uint32_t *positions,
-                                    const uint32_t *kept_table, uint32_t rows, uint32_t heads,
-                                    uint32_t kv_heads, uint32_t width, uint32_t keys,
-                                    uint32_t kept_pages, uint32_t page, float eps, float theta,
-                                    void *stream);
+typedef struct {
+    const float *qkv, *q_gain, *k_gain;                  /* reads */
+    float *q_out;                                        /* [rows, heads, width] */
+    void *k_cache, *v_cache;                             /* kept rows, bf16 (written) */
+    const uint32_t *slots, *positions, *kept_table;      /* kept_table may be NULL (dense) */
+    uint32_t rows, heads, kv_heads, width, keys, kept_pages, page;
+    float eps, theta;
+} ts_qk_args;
+int tessera_hip_qk_norm_rope_append(const ts_qk_args *a, void *stream);
 
 /* Embedding rows: out[r, :] = f32(table[ids[r] - first, :]), zeros outside the
  * table. table bf16 [rows_in_table, width].
  * Replaces: "gather" (engine/rules/kernels/src/gather.rs; interp cpu.rs:511-525). */
-int tessera_hip_gather(const void *table, const uint32_t *ids, float *out, uint32_t count,
-                       uint32_t table_rows, uint32_t width, uint32_t first, void *stream);
+typedef struct {
+    const void *table;    /* bf16 [table_rows, width] */
+    const uint32_t *ids;  /* [count] */
+    float *out;           /* [count, width] */
+    uint32_t count, table_rows, width, first;
+} ts_gather_args;
+int tessera_hip_gather(const ts_gather_args *a, void *stream);
 
 /* out[j] = x[j / picks, ids[j]], zero when ids[j] >= width; x [rows, width],
  * ids/out [rows, picks]. Replaces: interp take (engine/ir/interp/src/cpu.rs:498-508)
  * as the MoE layer uses it (engine/models/src/decoder.rs:78). */
-int tessera_hip_take(const float *x, const uint32_t *ids, float *out, uint32_t rows, uint32_t width,
-                     uint32_t picks, void *stream);
+typedef struct {
+    const float *x;       /* [rows, width] */
+    const uint32_t *ids;  /* [rows, picks] */
+    float *out;           /* [rows, picks] */
+    uint32_t rows, width, picks;
+} ts_take_args;
+int tessera_hip_take(const ts_take_args *a, void *stream);
 
 /* Row softmax in the reference's order: max from -inf (NaN ignored), exp(v - max),
  * sequential sum, divide. One thread per row: routing widths (<= 4096).
  * Replaces: interp softmax (engine/ir/interp/src/cpu.rs:49-59). out may alias x. */
-int tessera_hip_softmax(const float *x, float *out, uint32_t rows, uint32_t width, void *stream);
+typedef struct {
+    const float *x;  /* [rows, width] */
+    float *out;      /* [rows, width], may alias x */
+    uint32_t rows, width;
+} ts_softmax_args;
+int tessera_hip_softmax(const ts_softmax_args *a, void *stream);
 
 /* out[o, i] = sum_t x[o, t, i] * weights[o, t] (t in order from 0, no fused
  * multiply-add: bit-exact), or the mean when weights is NULL. x [outer, count, inner].
  * Replaces: mean / mix (engine/ir/interp/src/cpu.rs:450-473), the MoE combine. */
-int tessera_hip_mix(const float *x, const float *weights, float *out, uint32_t outer, uint32_t count,
-                    uint32_t inner, void *stream);
+typedef struct {
+    const float *x, *weights;  /* [outer, count, inner], [outer, count] or NULL (mean) */
+    float *out;                /* [outer, inner] */
+    uint32_t outer, count, inner;
+} ts_mix_args;
+int tessera_hip_mix(const ts_mix_args *a, void *stream);
 
 /* ids[r] = first index of the largest finite entry of row r (NaN and -inf
  * skipped; `width` when none). x f32 [rows, width].
  * Replaces: "peaks" + "argmax" (engine/rules/kernels/src/argmax.rs:74-129). */
-int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, uint32_t width,
-                       void *workspace, size_t workspace_bytes, void *stream);
-size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width);
+typedef struct {
+    const float *x;  /* [rows, width] */
+    uint32_t *ids;   /* [rows] */
+    void *workspace;
+    size_t workspace_bytes;
+    uint32_t rows, width;
+} ts_argmax_args;
+int tessera_hip_argmax(const ts_argmax_args *a, void *stream);
+size_t tessera_hip_argmax_workspace(const ts_argmax_args *a);
 
 /* ids[r] from the keys a product with TS_AFTER_ARGMAX folded (the same pick as
  * tessera_hip_argmax over its output row: first index of the largest entry, NaN and
  * -inf skipped, `width` when none), then keys[r] = 0 for the next product.
  * No counterpart in the reference: argmax fused into the lm_head product, so the
  * logits are not read back (engine/rules/kernels/src/argmax.rs:74-129 reads them). */
-int tessera_hip_argmax_keys(uint64_t *keys, uint32_t *ids, uint32_t rows, uint32_t width, void *stream);
+typedef struct {
+    uint64_t *keys;  /* [rows]: read, then cleared */
+    uint32_t *ids;   /* [rows] */
+    uint32_t rows, width;
+} ts_keys_args;
+int tessera_hip_argmax_keys(const ts_keys_args *a, void *stream);
 
 /* ids[r, 0..k): the row's k largest finite entries, best first, ties to the
  * lower index, NaN/-inf skipped, spare slots = width. x f32 [rows, width],
  * width <= 1024, k <= 32.
  * Replaces: "top_k" (engine/rules/kernels/src/argmax.rs:39-72; interp run.rs:577-591). */
-int tessera_hip_top_k(const float *x, uint32_t *ids, uint32_t rows, uint32_t width, uint32_t k,
-                      void *stream);
+typedef struct {
+    const float *x;  /* [rows, width] */
+    uint32_t *ids;   /* [rows, k] */
+    uint32_t rows, width, k;
+} ts_top_k_args;
+int tessera_hip_top_k(const ts_top_k_args *a, void *stream);
 
 #ifdef __cplusplus
 }

@@ -70,6 +70,45 @@ class PickedArgs(C.Structure):
     ]
 
 
+def _args(name, doc, fields):
+    """A ctypes Structure for one of the row stages' argument structs."""
+    return type(name, (C.Structure,), {"__doc__": doc + " (include/tessera_hip.h).", "_fields_": fields})
+
+
+_v, _u, _f = C.c_void_p, C.c_uint32, C.c_float
+NormArgs = _args("NormArgs", "ts_norm_args", [
+    ("x", _v), ("gain", _v), ("out", _v), ("rows", _u), ("width", _u), ("eps", _f)])
+RopeArgs = _args("RopeArgs", "ts_rope_args", [
+    ("x", _v), ("positions", _v), ("rows", _u), ("heads", _u), ("width", _u), ("theta", _f),
+    ("halves", C.c_int32)])
+AnglesArgs = _args("AnglesArgs", "ts_angles_args", [
+    ("table", _v), ("positions", _u), ("width", _u), ("theta", _f)])
+QkArgs = _args("QkArgs", "ts_qk_args", [
+    ("qkv", _v), ("q_gain", _v), ("k_gain", _v), ("q_out", _v), ("k_cache", _v), ("v_cache", _v),
+    ("slots", _v), ("positions", _v), ("kept_table", _v), ("rows", _u), ("heads", _u),
+    ("kv_heads", _u), ("width", _u), ("keys", _u), ("kept_pages", _u), ("page", _u),
+    ("eps", _f), ("theta", _f)])
+GatherArgs = _args("GatherArgs", "ts_gather_args", [
+    ("table", _v), ("ids", _v), ("out", _v), ("count", _u), ("table_rows", _u), ("width", _u),
+    ("first", _u)])
+TakeArgs = _args("TakeArgs", "ts_take_args", [
+    ("x", _v), ("ids", _v), ("out", _v), ("rows", _u), ("width", _u), ("picks", _u)])
+SoftmaxArgs = _args("SoftmaxArgs", "ts_softmax_args", [
+    ("x", _v), ("out", _v), ("rows", _u), ("width", _u)])
+MixArgs = _args("MixArgs", "ts_mix_args", [
+    ("x", _v), ("weights", _v), ("out", _v), ("outer", _u), ("count", _u), ("inner", _u)])
+ArgmaxArgs = _args("ArgmaxArgs", "ts_argmax_args", [
+    ("x", _v), ("ids", _v), ("workspace", _v), ("workspace_bytes", C.c_size_t), ("rows", _u),
+    ("width", _u)])
+KeysArgs = _args("KeysArgs", "ts_keys_args", [
+    ("keys", _v), ("ids", _v), ("rows", _u), ("width", _u)])
+TopKArgs = _args("TopKArgs", "ts_top_k_args", [
+    ("x", _v), ("ids", _v), ("rows", _u), ("width", _u), ("k", _u)])
+StepArgs = _args("StepArgs", "ts_step_args", [
+    ("rows", RowsArgs), ("qkv", _v), ("q_gain", _v), ("k_gain", _v), ("rope_table", _v),
+    ("rope_rows", _u), ("eps", _f)])
+
+
 _P = C.c_void_p
 _U = C.c_uint32
 _LA = C.POINTER(LinearArgs)
@@ -87,24 +126,24 @@ SIGNATURES = {
     "tessera_hip_tiled": (C.c_int, [_LA, _P]),
     "tessera_hip_picked": (C.c_int, [_PA, _P]),
     "tessera_hip_picked_workspace": (C.c_size_t, [_PA]),
-    "tessera_hip_take": (C.c_int, [_P, _P, _P, _U, _U, _U, _P]),
-    "tessera_hip_softmax": (C.c_int, [_P, _P, _U, _U, _P]),
-    "tessera_hip_mix": (C.c_int, [_P, _P, _P, _U, _U, _U, _P]),
+    "tessera_hip_take": (C.c_int, [C.POINTER(TakeArgs), _P]),
+    "tessera_hip_softmax": (C.c_int, [C.POINTER(SoftmaxArgs), _P]),
+    "tessera_hip_mix": (C.c_int, [C.POINTER(MixArgs), _P]),
     "tessera_hip_attend_rows": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_workspace": (C.c_size_t, [_RA]),
     "tessera_hip_attend_rows_noalloc": (C.c_int, [_RA, _P]),
     "tessera_hip_attend_rows_noalloc_limit": (C.c_size_t, []),
     "tessera_hip_flash_rows": (C.c_int, [_RA, _P]),
-    "tessera_hip_attend_step": (C.c_int, [_RA, _P, _P, _P, _P, _U, C.c_float, _P]),
-    "tessera_hip_rope_table": (C.c_int, [_P, _U, _U, C.c_float, _P]),
-    "tessera_hip_rms_norm": (C.c_int, [_P, _P, _P, _U, _U, C.c_float, _P]),
-    "tessera_hip_rope": (C.c_int, [_P, _P, _U, _U, _U, C.c_float, C.c_int32, _P]),
-    "tessera_hip_qk_norm_rope_append": (C.c_int, [_P] * 9 + [_U] * 7 + [C.c_float, C.c_float, _P]),
-    "tessera_hip_gather": (C.c_int, [_P, _P, _P, _U, _U, _U, _U, _P]),
-    "tessera_hip_argmax": (C.c_int, [_P, _P, _U, _U, _P, C.c_size_t, _P]),
-    "tessera_hip_argmax_workspace": (C.c_size_t, [_U, _U]),
-    "tessera_hip_argmax_keys": (C.c_int, [_P, _P, _U, _U, _P]),
-    "tessera_hip_top_k": (C.c_int, [_P, _P, _U, _U, _U, _P]),
+    "tessera_hip_attend_step": (C.c_int, [C.POINTER(StepArgs), _P]),
+    "tessera_hip_rope_table": (C.c_int, [C.POINTER(AnglesArgs), _P]),
+    "tessera_hip_rms_norm": (C.c_int, [C.POINTER(NormArgs), _P]),
+    "tessera_hip_rope": (C.c_int, [C.POINTER(RopeArgs), _P]),
+    "tessera_hip_qk_norm_rope_append": (C.c_int, [C.POINTER(QkArgs), _P]),
+    "tessera_hip_gather": (C.c_int, [C.POINTER(GatherArgs), _P]),
+    "tessera_hip_argmax": (C.c_int, [C.POINTER(ArgmaxArgs), _P]),
+    "tessera_hip_argmax_workspace": (C.c_size_t, [C.POINTER(ArgmaxArgs)]),
+    "tessera_hip_argmax_keys": (C.c_int, [C.POINTER(KeysArgs), _P]),
+    "tessera_hip_top_k": (C.c_int, [C.POINTER(TopKArgs), _P]),
 }
 
 

@@ -767,9 +767,12 @@ extern "C" int tessera_hip_attend_rows(const ts_rows_args *a, void *stream) {
     return launch_rows<false>(a, p, stream);
 }
 
-extern "C" int tessera_hip_attend_step(const ts_rows_args *a, const float *qkv, const float *q_gain,
-                                       const float *k_gain, const float *rope_table, uint32_t rope_rows, float eps,
-                                       void *stream) {
+extern "C" int tessera_hip_attend_step(const ts_step_args *s, void *stream) {
+    TS_REQUIRE(s, "attend_step: null args");
+    const ts_rows_args *a = &s->rows;
+    const float *qkv = s->qkv, *q_gain = s->q_gain, *k_gain = s->k_gain, *rope_table = s->rope_table;
+    const uint32_t rope_rows = s->rope_rows;
+    const float eps = s->eps;
     TS_REQUIRE(a && qkv && q_gain && k_gain && rope_table, "attend_step: null pointer");
     TS_REQUIRE(a->max_position < rope_rows, "attend_step: positions up to %u but the angle table has %u rows",
                a->max_position, rope_rows);

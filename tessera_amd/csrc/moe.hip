@@ -217,8 +217,12 @@ int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n
 
 }  // namespace ts
 
-extern "C" int tessera_hip_take(const float *x, const uint32_t *ids, float *out, uint32_t rows, uint32_t width,
-                                uint32_t picks, void *stream) {
+extern "C" int tessera_hip_take(const ts_take_args *a, void *stream) {
+    TS_REQUIRE(a, "take: null args");
+    const float *x = a->x;
+    const uint32_t *ids = a->ids;
+    float *out = a->out;
+    const uint32_t rows = a->rows, width = a->width, picks = a->picks;
     TS_REQUIRE(x && ids && out, "take: null pointer");
     const uint64_t total = (uint64_t)rows * picks;
     if (total == 0) return TS_OK;
@@ -229,7 +233,11 @@ extern "C" int tessera_hip_take(const float *x, const uint32_t *ids, float *out,
     return TS_OK;
 }
 
-extern "C" int tessera_hip_softmax(const float *x, float *out, uint32_t rows, uint32_t width, void *stream) {
+extern "C" int tessera_hip_softmax(const ts_softmax_args *a, void *stream) {
+    TS_REQUIRE(a, "softmax: null args");
+    const float *x = a->x;
+    float *out = a->out;
+    const uint32_t rows = a->rows, width = a->width;
     TS_REQUIRE(x && out, "softmax: null pointer");
     TS_REQUIRE(width >= 1 && width <= 4096, "softmax: width %u (routing widths, 1..4096)", width);
     if (rows == 0) return TS_OK;
@@ -239,8 +247,11 @@ extern "C" int tessera_hip_softmax(const float *x, float *out, uint32_t rows, ui
     return TS_OK;
 }
 
-extern "C" int tessera_hip_mix(const float *x, const float *weights, float *out, uint32_t outer, uint32_t count,
-                               uint32_t inner, void *stream) {
+extern "C" int tessera_hip_mix(const ts_mix_args *a, void *stream) {
+    TS_REQUIRE(a, "mix: null args");
+    const float *x = a->x, *weights = a->weights;
+    float *out = a->out;
+    const uint32_t outer = a->outer, count = a->count, inner = a->inner;
     TS_REQUIRE(x && out, "mix: null pointer");
     TS_REQUIRE(count >= 1, "mix: count 0");
     const uint64_t total = (uint64_t)outer * inner;

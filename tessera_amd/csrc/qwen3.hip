@@ -191,18 +191,21 @@ int run_layers(ts_qwen3 *m, uint32_t rows, const uint32_t *slots, const uint32_t
             a.stages = TS_BEFORE_RMS_NORM;
             a.gain = L.ln1;
         } else {
-            TRY(tessera_hip_rms_norm(m->x, L.ln1, m->xn, rows, H, c.eps, s));
+            const ts_norm_args n = {m->x, L.ln1, m->xn, rows, H, c.eps};
+            TRY(tessera_hip_rms_norm(&n, s));
         }
         TRY(tessera_hip_linear(&a, s));
         ts_rows_args r = rows_args(m, L, rows, slots, pos, max_position);
         if (rows == 1) {
             // q/k norm, RoPE, the kept-row append and attention in one launch (a row
             // may only read keys appended by earlier launches, so one row per slot).
-            TRY(tessera_hip_attend_step(&r, m->qkv, L.q_norm, L.k_norm, m->rope, c.max_context, c.eps, s));
+            const ts_step_args st = {r, m->qkv, L.q_norm, L.k_norm, m->rope, c.max_context, c.eps};
+            TRY(tessera_hip_attend_step(&st, s));
         } else {
-            TRY(tessera_hip_qk_norm_rope_append(m->qkv, L.q_norm, L.k_norm, m->q, L.k_cache, L.v_cache, slots,
-                                                pos, m->d_table, rows, c.heads, c.kv_heads, D,
-                                                m->kept_pages * c.page, m->kept_pages, c.page, c.eps, c.theta, s));
+            const ts_qk_args q = {m->qkv, L.q_norm, L.k_norm, m->q, L.k_cache, L.v_cache, slots, pos,
+                                  m->d_table, rows, c.heads, c.kv_heads, D, m->kept_pages * c.page,
+                                  m->kept_pages, c.page, c.eps, c.theta};
+            TRY(tessera_hip_qk_norm_rope_append(&q, s));
             TRY(fused ? tessera_hip_attend_rows(&r, s) : tessera_hip_flash_rows(&r, s));
         }
         a = lin(m->attn, L.o, m->x, rows, H, QD, m);
@@ -215,7 +218,8 @@ int run_layers(ts_qwen3 *m, uint32_t rows, const uint32_t *slots, const uint32_t
             a.stages |= TS_BEFORE_RMS_NORM;
             a.gain = L.ln2;
         } else {
-            TRY(tessera_hip_rms_norm(m->x, L.ln2, m->xn, rows, H, c.eps, s));
+            const ts_norm_args n = {m->x, L.ln2, m->xn, rows, H, c.eps};
+            TRY(tessera_hip_rms_norm(&n, s));
         }
         TRY(tessera_hip_linear(&a, s));
         a = lin(m->h, L.down, m->x, rows, H, c.ffn, m);
@@ -240,7 +244,8 @@ int head(ts_qwen3 *m, uint32_t row) {
 
 int decode_step(ts_qwen3 *m) {
     const ts_qwen3_config &c = m->c;
-    TRY(tessera_hip_gather(m->embed, m->d_tok, m->x, 1, c.vocab, c.hidden, 0, m->stream));
+    const ts_gather_args g = {m->embed, m->d_tok, m->x, 1, c.vocab, c.hidden, 0};
+    TRY(tessera_hip_gather(&g, m->stream));
     TRY(run_layers(m, 1, m->d_slot, m->d_pos, c.max_context - 1));
     TRY(head(m, 0));
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, m->stream, m->d_key, m->d_tok, m->d_pos, m->d_hist,
@@ -275,7 +280,10 @@ int launch_step(ts_qwen3 *m, uint32_t steps) {
 
 size_t workspace_need(ts_qwen3 *m) {
     const ts_qwen3_config &c = m->c;
-    size_t need = tessera_hip_argmax_workspace(1, c.vocab);
+    ts_argmax_args am{};
+    am.rows = 1;
+    am.width = c.vocab;
+    size_t need = tessera_hip_argmax_workspace(&am);
     const uint32_t H = c.hidden, D = c.head_dim;
     const uint32_t shapes[][2] = {{(c.heads + 2 * c.kv_heads) * D, H}, {H, c.heads * D}, {c.ffn, H},
                                   {H, c.ffn}, {c.vocab, H}};
@@ -377,7 +385,8 @@ extern "C" int tessera_qwen3_open(const ts_qwen3_config *cfg, uint64_t seed, ts_
         if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
         if (e != hipSuccess) return fail(ts::hip_status(e, "buffer list upload"));
     }
-    if ((rc = tessera_hip_rope_table(m->rope, c.max_context, D, c.theta, m->stream))) return fail(rc);
+    const ts_angles_args angles = {m->rope, c.max_context, D, c.theta};
+    if ((rc = tessera_hip_rope_table(&angles, m->stream))) return fail(rc);
     m->ws_bytes = workspace_need(m);
     if (m->ws_bytes) {
         char *w = nullptr;
@@ -519,7 +528,8 @@ extern "C" int tessera_qwen3_prefill(ts_qwen3 *m, const uint32_t *tokens, uint32
     if (e == hipSuccess) e = hipMemcpyAsync(m->d_prompt, tokens, count * 4, hipMemcpyHostToDevice, m->stream);
     if (e != hipSuccess) return ts::hip_status(e, "prefill upload");
     const ts_qwen3_config &c = m->c;
-    TRY(tessera_hip_gather(m->embed, m->d_prompt, m->x, count, c.vocab, c.hidden, 0, m->stream));
+    const ts_gather_args g = {m->embed, m->d_prompt, m->x, count, c.vocab, c.hidden, 0};
+    TRY(tessera_hip_gather(&g, m->stream));
     TRY(run_layers(m, count, m->d_prompt_slot, m->d_prompt_pos, count - 1));
     TRY(head(m, count - 1));
     hipLaunchKernelGGL(start_kernel, dim3(1), dim3(1), 0, m->stream, m->d_key, m->d_tok, m->d_pos, m->d_hist, count,

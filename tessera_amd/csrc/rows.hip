@@ -233,8 +233,12 @@ __global__ __launch_bounds__(256) void top_k_kernel(const float *x, uint32_t *id
 
 }  // namespace
 
-extern "C" int tessera_hip_rms_norm(const float *x, const float *gain, float *out, uint32_t rows, uint32_t width,
-                                    float eps, void *stream) {
+extern "C" int tessera_hip_rms_norm(const ts_norm_args *a, void *stream) {
+    TS_REQUIRE(a, "rms_norm: null args");
+    const float *x = a->x, *gain = a->gain;
+    float *out = a->out;
+    const uint32_t rows = a->rows, width = a->width;
+    const float eps = a->eps;
     TS_REQUIRE(x && gain && out, "rms_norm: null pointer");
     TS_REQUIRE(width >= 1, "rms_norm: width 0");
     if (rows == 0) return TS_OK;
@@ -244,8 +248,13 @@ extern "C" int tessera_hip_rms_norm(const float *x, const float *gain, float *ou
     return TS_OK;
 }
 
-extern "C" int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t rows, uint32_t heads,
-                                uint32_t width, float theta, int32_t halves, void *stream) {
+extern "C" int tessera_hip_rope(const ts_rope_args *a, void *stream) {
+    TS_REQUIRE(a, "rope: null args");
+    float *x = a->x;
+    const uint32_t *positions = a->positions;
+    const uint32_t rows = a->rows, heads = a->heads, width = a->width;
+    const float theta = a->theta;
+    const int32_t halves = a->halves;
     TS_REQUIRE(x && positions, "rope: null pointer");
     TS_REQUIRE(width >= 2 && width % 2 == 0, "rope: width %u must be even", width);
     const uint64_t total = (uint64_t)rows * heads * (width / 2);
@@ -256,7 +265,11 @@ extern "C" int tessera_hip_rope(float *x, const uint32_t *positions, uint32_t ro
     return TS_OK;
 }
 
-extern "C" int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t width, float theta, void *stream) {
+extern "C" int tessera_hip_rope_table(const ts_angles_args *a, void *stream) {
+    TS_REQUIRE(a, "rope_table: null args");
+    float *table = a->table;
+    const uint32_t positions = a->positions, width = a->width;
+    const float theta = a->theta;
     TS_REQUIRE(table, "rope_table: null pointer");
     TS_REQUIRE(width >= 2 && width % 2 == 0, "rope_table: width %u must be even", width);
     const uint64_t n = (uint64_t)positions * (width / 2);
@@ -267,12 +280,15 @@ extern "C" int tessera_hip_rope_table(float *table, uint32_t positions, uint32_t
     return TS_OK;
 }
 
-extern "C" int tessera_hip_qk_norm_rope_append(const float *qkv, const float *q_gain, const float *k_gain,
-                                               float *q_out, void *k_cache, void *v_cache, const uint32_t *slots,
-                                               const uint32_t *positions, const uint32_t *kept_table,
-                                               uint32_t rows, uint32_t heads, uint32_t kv_heads, uint32_t width,
-                                               uint32_t keys, uint32_t kept_pages, uint32_t page, float eps,
-                                               float theta, void *stream) {
+extern "C" int tessera_hip_qk_norm_rope_append(const ts_qk_args *a, void *stream) {
+    TS_REQUIRE(a, "qk_norm_rope_append: null args");
+    const float *qkv = a->qkv, *q_gain = a->q_gain, *k_gain = a->k_gain;
+    float *q_out = a->q_out;
+    void *k_cache = a->k_cache, *v_cache = a->v_cache;
+    const uint32_t *slots = a->slots, *positions = a->positions, *kept_table = a->kept_table;
+    const uint32_t rows = a->rows, heads = a->heads, kv_heads = a->kv_heads, width = a->width, keys = a->keys;
+    const uint32_t kept_pages = a->kept_pages, page = a->page;
+    const float eps = a->eps, theta = a->theta;
     TS_REQUIRE(qkv && q_gain && k_gain && q_out && k_cache && v_cache && slots && positions,
                "qk_norm_rope_append: null pointer");
     TS_REQUIRE(width == 128, "qk_norm_rope_append: head width %u (128 supported)", width);
@@ -293,8 +309,12 @@ extern "C" int tessera_hip_qk_norm_rope_append(const float *qkv, const float *q_
     return TS_OK;
 }
 
-extern "C" int tessera_hip_gather(const void *table, const uint32_t *ids, float *out, uint32_t count,
-                                  uint32_t table_rows, uint32_t width, uint32_t first, void *stream) {
+extern "C" int tessera_hip_gather(const ts_gather_args *a, void *stream) {
+    TS_REQUIRE(a, "gather: null args");
+    const void *table = a->table;
+    const uint32_t *ids = a->ids;
+    float *out = a->out;
+    const uint32_t count = a->count, table_rows = a->table_rows, width = a->width, first = a->first;
     TS_REQUIRE(table && ids && out, "gather: null pointer");
     if (count == 0 || width == 0) return TS_OK;
     TS_REQUIRE(count <= 65535, "gather: %u rows (at most 65535 per call)", count);
@@ -312,7 +332,11 @@ __global__ void argmax_keys_kernel(uint64_t *keys, uint32_t *ids, uint32_t rows,
     keys[r] = 0;
 }
 
-extern "C" int tessera_hip_argmax_keys(uint64_t *keys, uint32_t *ids, uint32_t rows, uint32_t width, void *stream) {
+extern "C" int tessera_hip_argmax_keys(const ts_keys_args *a, void *stream) {
+    TS_REQUIRE(a, "argmax_keys: null args");
+    uint64_t *keys = a->keys;
+    uint32_t *ids = a->ids;
+    const uint32_t rows = a->rows, width = a->width;
     TS_REQUIRE(keys && ids, "argmax_keys: null pointer");
     if (rows == 0) return TS_OK;
     hipLaunchKernelGGL(argmax_keys_kernel, dim3((rows + 255) / 256), dim3(256), 0, (hipStream_t)stream, keys, ids,
@@ -321,18 +345,25 @@ extern "C" int tessera_hip_argmax_keys(uint64_t *keys, uint32_t *ids, uint32_t r
     return TS_OK;
 }
 
-extern "C" size_t tessera_hip_argmax_workspace(uint32_t rows, uint32_t width) {
+extern "C" size_t tessera_hip_argmax_workspace(const ts_argmax_args *a) {
+    if (!a) return 0;
+    const uint32_t rows = a->rows, width = a->width;
     const size_t spans = (width + kSpan - 1) / kSpan;
     return (size_t)rows * spans * (sizeof(float) + sizeof(uint32_t));
 }
 
-extern "C" int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, uint32_t width, void *workspace,
-                                  size_t workspace_bytes, void *stream) {
+extern "C" int tessera_hip_argmax(const ts_argmax_args *a, void *stream) {
+    TS_REQUIRE(a, "argmax: null args");
+    const float *x = a->x;
+    uint32_t *ids = a->ids;
+    const uint32_t rows = a->rows, width = a->width;
+    void *workspace = a->workspace;
+    const size_t workspace_bytes = a->workspace_bytes;
     TS_REQUIRE(x && ids, "argmax: null pointer");
     TS_REQUIRE(width >= 1, "argmax: width 0");
     if (rows == 0) return TS_OK;
     TS_REQUIRE(rows <= 65535, "argmax: %u rows (at most 65535)", rows);
-    const size_t need = tessera_hip_argmax_workspace(rows, width);
+    const size_t need = tessera_hip_argmax_workspace(a);
     if (!workspace || workspace_bytes < need)
         return ts::fail(TS_ERR_WORKSPACE, "argmax: workspace of %zu bytes needed", need);
     const uint32_t spans = (width + kSpan - 1) / kSpan;
@@ -346,8 +377,11 @@ extern "C" int tessera_hip_argmax(const float *x, uint32_t *ids, uint32_t rows, 
     return TS_OK;
 }
 
-extern "C" int tessera_hip_top_k(const float *x, uint32_t *ids, uint32_t rows, uint32_t width, uint32_t k,
-                                 void *stream) {
+extern "C" int tessera_hip_top_k(const ts_top_k_args *a, void *stream) {
+    TS_REQUIRE(a, "top_k: null args");
+    const float *x = a->x;
+    uint32_t *ids = a->ids;
+    const uint32_t rows = a->rows, width = a->width, k = a->k;
     TS_REQUIRE(x && ids, "top_k: null pointer");
     TS_REQUIRE(width >= 1 && width <= 1024, "top_k: width %u outside 1..1024", width);
     TS_REQUIRE(k >= 1 && k <= 1024, "top_k: k %u", k);

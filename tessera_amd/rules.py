@@ -134,7 +134,7 @@ def take(x, ids, out=None):
     picks = ids.shape[-1]
     if out is None:
         out = torch.empty(ids.shape, dtype=torch.float32, device=x.device)
-    abi.call("tessera_hip_take", _ptr(x), _ptr(ids), _ptr(out), rows, width, picks, _stream())
+    abi.call("tessera_hip_take", C.byref(abi.TakeArgs(_ptr(x), _ptr(ids), _ptr(out), rows, width, picks)), _stream())
     return out
 
 
@@ -143,7 +143,7 @@ def softmax(x, out=None):
     rows = x.numel() // width
     if out is None:
         out = torch.empty_like(x)
-    abi.call("tessera_hip_softmax", _ptr(x), _ptr(out), rows, width, _stream())
+    abi.call("tessera_hip_softmax", C.byref(abi.SoftmaxArgs(_ptr(x), _ptr(out), rows, width)), _stream())
     return out
 
 
@@ -153,7 +153,8 @@ def mix(x, weights=None, out=None):
     inner = x.numel() // (outer * count)
     if out is None:
         out = torch.empty((outer,) + tuple(x.shape[2:]), dtype=torch.float32, device=x.device)
-    abi.call("tessera_hip_mix", _ptr(x), _ptr(weights), _ptr(out), outer, count, inner, _stream())
+    abi.call("tessera_hip_mix", C.byref(abi.MixArgs(_ptr(x), _ptr(weights), _ptr(out), outer, count, inner)),
+             _stream())
     return out
 
 
@@ -211,7 +212,7 @@ def attend_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_page
 def rope_table(positions, theta, width=128, device="cuda"):
     """(cos, sin) of every (position, pair) angle (the "angles" stage)."""
     t = torch.empty((positions, width // 2, 2), dtype=torch.float32, device=device)
-    abi.call("tessera_hip_rope_table", _ptr(t), positions, width, C.c_float(theta), _stream())
+    abi.call("tessera_hip_rope_table", C.byref(abi.AnglesArgs(_ptr(t), positions, width, theta)), _stream())
     return t
 
 
@@ -228,8 +229,8 @@ def attend_step(qkv, q_gain, k_gain, k, v, slots, positions, *, heads, keys, sca
                   kept_pages=kept_pages, page=page, back=back, max_position=max_position)
     need = abi.load().tessera_hip_attend_rows_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(qkv.device).get(need)
-    abi.call("tessera_hip_attend_step", C.byref(a), _ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(angles),
-             angles.shape[0], C.c_float(eps), _stream())
+    st = abi.StepArgs(a, _ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(angles), angles.shape[0], eps)
+    abi.call("tessera_hip_attend_step", C.byref(st), _stream())
     return out
 
 
@@ -250,24 +251,26 @@ def rms_norm(x, gain, eps, out=None):
     rows, width = x.reshape(-1, x.shape[-1]).shape
     if out is None:
         out = torch.empty_like(x)
-    abi.call("tessera_hip_rms_norm", _ptr(x), _ptr(gain), _ptr(out), rows, width, C.c_float(eps), _stream())
+    abi.call("tessera_hip_rms_norm", C.byref(abi.NormArgs(_ptr(x), _ptr(gain), _ptr(out), rows, width, eps)),
+             _stream())
     return out
 
 
 def rope(x, positions, theta, halves=True):
     """In place on x [rows, heads, width]."""
     rows, heads, width = x.shape
-    abi.call("tessera_hip_rope", _ptr(x), _ptr(positions), rows, heads, width, C.c_float(theta),
-             1 if halves else 0, _stream())
+    a = abi.RopeArgs(_ptr(x), _ptr(positions), rows, heads, width, theta, 1 if halves else 0)
+    abi.call("tessera_hip_rope", C.byref(a), _stream())
     return x
 
 
 def qk_norm_rope_append(qkv, q_gain, k_gain, q_out, k_cache, v_cache, slots, positions, *, heads,
                         kv_heads, keys, eps, theta, table=None, kept_pages=0, page=16):
     rows = qkv.shape[0]
-    abi.call("tessera_hip_qk_norm_rope_append", _ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(q_out),
-             _ptr(k_cache), _ptr(v_cache), _ptr(slots), _ptr(positions), _ptr(table), rows, heads, kv_heads,
-             128, keys, kept_pages, page, C.c_float(eps), C.c_float(theta), _stream())
+    a = abi.QkArgs(_ptr(qkv), _ptr(q_gain), _ptr(k_gain), _ptr(q_out), _ptr(k_cache), _ptr(v_cache),
+                   _ptr(slots), _ptr(positions), _ptr(table), rows, heads, kv_heads, 128, keys, kept_pages,
+                   page, eps, theta)
+    abi.call("tessera_hip_qk_norm_rope_append", C.byref(a), _stream())
     return q_out
 
 
@@ -276,7 +279,8 @@ def gather(table, ids, first=0, out=None):
     rows, width = table.shape
     if out is None:
         out = torch.empty((count, width), dtype=torch.float32, device=table.device)
-    abi.call("tessera_hip_gather", _ptr(table), _ptr(ids), _ptr(out), count, rows, width, first, _stream())
+    a = abi.GatherArgs(_ptr(table), _ptr(ids), _ptr(out), count, rows, width, first)
+    abi.call("tessera_hip_gather", C.byref(a), _stream())
     return out
 
 
@@ -284,9 +288,9 @@ def argmax(x, ids=None):
     rows, width = x.shape
     if ids is None:
         ids = torch.empty(rows, dtype=torch.int32, device=x.device)
-    need = abi.load().tessera_hip_argmax_workspace(rows, width)
-    ws, nbytes = workspace(x.device).get(need)
-    abi.call("tessera_hip_argmax", _ptr(x), _ptr(ids), rows, width, ws, nbytes, _stream())
+    a = abi.ArgmaxArgs(_ptr(x), _ptr(ids), None, 0, rows, width)
+    a.workspace, a.workspace_bytes = workspace(x.device).get(abi.load().tessera_hip_argmax_workspace(C.byref(a)))
+    abi.call("tessera_hip_argmax", C.byref(a), _stream())
     return ids
 
 
@@ -302,7 +306,7 @@ def linear_argmax(x, w, *, gain=None, eps=1e-6, keys=None):
     a.workspace, a.workspace_bytes = _ptr(keys), keys.numel() * 8
     abi.call("tessera_hip_lanes", C.byref(a), _stream())
     ids = torch.empty(m, dtype=torch.int32, device=x.device)
-    abi.call("tessera_hip_argmax_keys", _ptr(keys), _ptr(ids), m, n, _stream())
+    abi.call("tessera_hip_argmax_keys", C.byref(abi.KeysArgs(_ptr(keys), _ptr(ids), m, n)), _stream())
     return out, ids
 
 
@@ -310,5 +314,5 @@ def top_k(x, k, ids=None):
     rows, width = x.shape
     if ids is None:
         ids = torch.empty((rows, k), dtype=torch.int32, device=x.device)
-    abi.call("tessera_hip_top_k", _ptr(x), _ptr(ids), rows, width, k, _stream())
+    abi.call("tessera_hip_top_k", C.byref(abi.TopKArgs(_ptr(x), _ptr(ids), rows, width, k)), _stream())
     return ids

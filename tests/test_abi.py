@@ -17,7 +17,7 @@ def test_exports_every_declared_function():
     arity = abi.declared_arity()
     for name, (_, args) in sigs.items():
         assert arity[name] == len(args), (name, arity[name], len(args))
-    assert lib.tessera_hip_abi_version() == 2
+    assert lib.tessera_hip_abi_version() == 3
 
 
 def test_argument_errors_need_no_device():
@@ -34,7 +34,9 @@ def test_argument_errors_need_no_device():
     r.width, r.heads, r.kv_heads = 64, 16, 8
     assert lib.tessera_hip_attend_rows(C.byref(r), None) == abi.TS_ERR_ARG
     assert b"width 64" in lib.tessera_hip_last_error()
-    assert lib.tessera_hip_top_k(None, None, 1, 4, 2, None) == abi.TS_ERR_ARG
+    assert lib.tessera_hip_top_k(None, None) == abi.TS_ERR_ARG
+    assert lib.tessera_hip_top_k(C.byref(abi.TopKArgs(None, None, 1, 4, 2)), None) == abi.TS_ERR_ARG
+    assert lib.tessera_hip_rms_norm(C.byref(abi.NormArgs(None, None, None, 1, 8, 1e-6)), None) == abi.TS_ERR_ARG
 
 
 def test_struct_layout_matches_header():
@@ -45,6 +47,41 @@ def test_struct_layout_matches_header():
     assert abi.RowsArgs.status.offset == 128 and C.sizeof(abi.RowsArgs) == 136
     assert C.sizeof(abi.PickedArgs) == 104
     assert abi.PickedArgs.rows.offset == 56 and abi.PickedArgs.stages.offset == 100
+
+
+STRUCTS = {
+    "ts_linear_args": "LinearArgs", "ts_rows_args": "RowsArgs", "ts_picked_args": "PickedArgs",
+    "ts_norm_args": "NormArgs", "ts_rope_args": "RopeArgs", "ts_angles_args": "AnglesArgs",
+    "ts_qk_args": "QkArgs", "ts_gather_args": "GatherArgs", "ts_take_args": "TakeArgs",
+    "ts_softmax_args": "SoftmaxArgs", "ts_mix_args": "MixArgs", "ts_argmax_args": "ArgmaxArgs",
+    "ts_keys_args": "KeysArgs", "ts_top_k_args": "TopKArgs", "ts_step_args": "StepArgs",
+}
+
+
+def test_every_struct_matches_the_compiler(tmp_path):
+    """Each binding Structure has the size and field offsets gcc gives the header's
+    struct of the same name."""
+    import shutil
+    import subprocess
+    import pytest
+    if shutil.which("gcc") is None:
+        pytest.skip("no gcc")
+    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{abi.HEADER}"', "int main(void) {"]
+    want = []
+    for cname, pname in STRUCTS.items():
+        st = getattr(abi, pname)
+        lines.append(f'printf("%zu\\n", sizeof({cname}));')
+        want.append(C.sizeof(st))
+        for field, _ in st._fields_:
+            lines.append(f'printf("%zu\\n", offsetof({cname}, {field}));')
+            want.append(getattr(st, field).offset)
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
+    assert got == want
 
 
 def test_workspace_sizes():
@@ -96,7 +133,8 @@ def test_attend_step_refuses_workspace_sized_for_attend_rows():
     r.scale, r.q_dtype, r.kv_dtype, r.out_dtype = 0.088, abi.TS_F32, abi.TS_BF16, abi.TS_F32
     r.max_position, r.keys = 2999, 188 * 16
     r.workspace_bytes = 1 * 8 * 6 * 2 * 130 * 4  # attend_rows' 6 partitions at this span
-    rc = lib.tessera_hip_attend_step(C.byref(r), fake, fake, fake, fake, 3000, C.c_float(1e-6), None)
+    st = abi.StepArgs(r, fake, fake, fake, fake, 3000, 1e-6)
+    rc = lib.tessera_hip_attend_step(C.byref(st), None)
     assert rc == abi.TS_ERR_WORKSPACE
 
 
