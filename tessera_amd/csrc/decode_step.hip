@@ -51,6 +51,7 @@ constexpr uint64_t kTimeout = 200000000ull;     // 2 s of the 100 MHz clock
 constexpr int kPre = 5;                         // 4-key blocks per wave per attention pass
 constexpr uint32_t kMaxLm = 1024;               // lm_head rows a group holds
 constexpr int kLmDepth = 4;                     // lm_head row tiles in flight per wave
+constexpr uint64_t kPrefetchDelay = 70;         // 0.7 us of the 100 MHz clock
 // 16-row tiles a group holds per product role (gate/up: gate tiles then up tiles).
 constexpr int kTilesQkv = 4, kTilesO = 2, kTilesGu = 4, kTilesDn = 2;
 
@@ -214,6 +215,15 @@ TS_DEV float poll1(Ctx &c, const uint64_t *src, uint32_t tag) {
     return __uint_as_float((uint32_t)w);
 }
 
+// Wait for one tagged word, every lane of the wave loading the same address (one
+// request a wave): the light wait before a heavy poll.
+TS_DEV void await(Ctx &c, const uint64_t *src, uint32_t tag) {
+    uint64_t t0 = 0;
+    uint32_t it = 0;
+    while ((uint32_t)(ld_tag(src) >> 32) != tag && spin(c, it, t0)) {
+    }
+}
+
 // Gains of the words this thread stages (1 without a gain), loaded before the poll.
 template <int NX>
 TS_DEV void gains(const Ctx &c, const float *g, uint32_t n, float (&gv)[NX]) {
@@ -340,7 +350,9 @@ TS_DEV void lm_rows(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t,
     {
         float v[2], gv[2];
         gains<2>(c, p.norm, H, gv);
-        poll<2>(c, p.hand + (size_t)(p.L - 1) * hd.block + hd.xo, H, tag, v);
+        const uint64_t *blk = p.hand + (size_t)(p.L - 1) * hd.block;
+        await(c, blk + hd.hf + c.wave * (p.F / kW), tag);  // the last gate/up first
+        poll<2>(c, blk + hd.xo, H, tag, v);
         stage<2>(c, v, H, gv);
     }
     mark(p, c, t, p.L, 0);
@@ -468,6 +480,7 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
         const char *P = (const char *)p.packed[l][KIND] + (size_t)idx * TILES * KSt * 1024;
 #pragma unroll
         for (int t = 0; t < TILES; t++) {
+
 #pragma unroll
             for (int j = 0; j < KS; j++) {
                 const uint32_t ks = c.wave * KS + j;
@@ -510,6 +523,14 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
             } else {
                 const uint64_t *in = KIND == kQkv ? prev + hd.xo
                                                   : (KIND == kO ? blk + hd.att : (KIND == kGu ? blk + hd.x2 : blk + hd.hf));
+                {
+                    // The stage before the input's producers: while it runs, one word a
+                    // wave is polled instead of the whole input.
+                    const uint64_t *pre = KIND == kQkv ? prev + hd.hf
+                                                       : (KIND == kO ? blk + hd.qkv : (KIND == kGu ? blk + hd.att : blk + hd.x2));
+                    const uint32_t pn = KIND == kQkv ? F : (KIND == kO ? QKV : (KIND == kGu ? QD : H));
+                    await(c, pre + c.wave * (pn / kW), tag);
+                }
                 poll<NX>(c, in, n, tag, v, res_src, &rv);
             }
             if (has_res) c.res()[c.tid] = rv;
@@ -582,6 +603,12 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
                 mark(p, c, t, l, 1);
                 // The next layer's tiles (the first layer's after the lm_head).
 #ifndef TS_NOPF
+                // Held back kPrefetchDelay first: issued at once, every role's prefetch
+                // lands in the hand-off that follows its publish and slows those polls.
+                {
+                    const uint64_t t0 = now();
+                    while (now() - t0 < kPrefetchDelay) __builtin_amdgcn_s_sleep(8);
+                }
                 if (l + 1 < p.L) load(l + 1);
 #endif
             }
