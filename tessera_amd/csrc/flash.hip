@@ -10,26 +10,26 @@
 // gfx950 design:
 //  * One group per (128 query rows, q heads of one kv head): 4 waves per q head, each
 //    wave owns 32 rows (two 16-query MFMA tiles); with GQA pairs a group of 8 waves
-//    covers both heads of the pair. Each K/V block is loaded and staged once for all
-//    of that MFMA work: the staging is VALU work, and VALU, not the matrix unit,
-//    bounds this kernel (64 rows and one head per group measured 1.8x slower).
+//    covers both heads of the pair. Each K/V block is loaded once for all of that
+//    MFMA work (64 rows and one head per group measured 1.8x slower).
 //  * Rows may be packed ragged (prompts back to back): a group whose rows belong to
 //    several slots makes one pass over the keys per distinct slot, in order of first
 //    appearance, as the reference's flash_rows does (flash.rs:504-591); a pass
 //    touches only its own rows' softmax state, and waves with none of them idle
 //    through it. The common case, one slot per group, is one pass.
-//  * Keys stream in 64-row blocks. K and V go to LDS as rows ([key][d], 16-byte
-//    chunks XOR-swizzled by key), 16 bytes per lane, no reshuffling: the V^T operand
-//    of O^T += V^T P^T comes out of LDS already transposed through gfx950's
-//    ds_read_b64_tr_b16 (a lane octet transpose on the VALU cost more than the
-//    softmax before this).
+//  * Keys stream in 64-row blocks, two resident in LDS: block b + 1's K and V rows go
+//    straight from memory to LDS (global_load_lds, no staging registers or LDS
+//    stores) while block b computes, one barrier per block. Rows sit in LDS as [key][d]
+//    with 16-byte chunks XOR-swizzled by key (the swizzle picks each lane's source
+//    chunk, since a wave's 1 KiB lands contiguously); the V^T operand of
+//    O^T += V^T P^T comes out of LDS already transposed through gfx950's
+//    ds_read_b64_tr_b16. Fragment offsets are computed once per lane.
 //  * The group's page-table entries are copied to LDS once.
 //  * S^T = K Q^T: 4 key tiles x 4 d-steps of v_mfma_f32_16x16x32_bf16 per q part
 //    (bf16 q as is; f32 q split into two exact bf16 parts). Online softmax per query
-//    in base 2; P^T (bf16; two parts for f32 q) feeds O^T += V^T P^T straight from
-//    registers (the layout notes at flash_rows_kernel).
-//  * The next key block's K/V loads are issued before the current block computes,
-//    and the barriers wait for LDS only, so HBM latency hides under the MFMAs.
+//    in base 2 with a lazy reference point (moved only when a score passes it by
+//    2^8, so most blocks skip rescaling O); P^T (bf16; two parts for f32 q) feeds
+//    O^T += V^T P^T straight from registers (the layout notes at flash_rows_kernel).
 #include "common.h"
 
 namespace {
@@ -37,6 +37,7 @@ namespace {
 constexpr int kQT = 2;              // 16-query tiles per wave
 constexpr int kRows = 64 * kQT;     // query rows per group (4 waves)
 constexpr int kKeys = 64;   // keys per block (two 32-key MFMA steps of P V)
+constexpr float kSlack = 8.0f;  // base-2 headroom of the softmax reference point
 
 struct FlashParams {
     const void *q;
@@ -63,29 +64,11 @@ TS_DEV uint64_t key_row(const FlashParams &p, uint32_t slot, uint32_t pos, const
                 : kept_row(p, slot, pos);
 }
 
-// K and V of one 64-key block in flight, 16 bytes (8 d values) per load, kC loads per
-// thread (1024 / kC threads). K: thread t holds key idx / 16, chunk idx % 16
-// (idx = t + 1024 / kC c); V likewise. Keys past the last row's position may sit in
-// pages never written: they load as zeros.
-template <int kC>
-TS_DEV void fetch_kv(const FlashParams &p, uint32_t slot, uint32_t kvh, uint32_t kb, uint32_t hi, const uint32_t *stab,
-                     uint32_t p0, u32x4 (&kr)[kC], u32x4 (&vr)[kC]) {
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int c = 0; c < kC; c++) {
-        const uint32_t idx = threadIdx.x + 1024 / kC * c, key = idx >> 4, chunk = idx & 15, pos = kb + key;
-        kr[c] = u32x4{0, 0, 0, 0};
-        if (pos <= hi && (p.table || pos < p.keys)) {
-            const uint64_t row = key_row(p, slot, pos, stab, p0);
-            kr[c] = *(const u32x4 *)(p.k + (row * p.kv_heads + kvh) * 128 + chunk * 8);
-        }
-        vr[c] = u32x4{0, 0, 0, 0};
-        if (pos <= hi && (p.table || pos < p.keys)) {
-            const uint64_t row = key_row(p, slot, pos, stab, p0);
-            vr[c] = *(const u32x4 *)(p.v + (row * p.kv_heads + kvh) * 128 + chunk * 8);
-        }
-    }
-}
+typedef __attribute__((address_space(3))) void flash_lds_void;
+
+// Bytes of one key block buffer in LDS: 64 K rows then 64 V rows of 256 bytes, the
+// 16-byte chunks of row key at chunk ^ (key & 15).
+constexpr uint32_t kBlockBytes = 2 * kKeys * 256;
 
 // Sums and maxima over the four 16-lane rows of a wave, in every lane (gfx950
 // permlane swaps: VALU).
@@ -109,9 +92,7 @@ TS_DEV float rows4_max(float x) {
 // k0 .. k0 + 3: four consecutive keys of one d, as the MFMA A operand wants.
 typedef short ts_v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) ts_v4i16 lds_v4i16;
-TS_DEV u32x2 read_vt4(const uint16_t (*sv)[128], uint32_t key, uint32_t d) {
-    const uint32_t chunk = d >> 3;
-    const uint16_t *a = &sv[key][((chunk ^ (key & 15)) << 3) + (d & 7)];
+TS_DEV u32x2 read_vt4(const char *a) {
     const ts_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16 *)a);
     return __builtin_bit_cast(u32x2, v);
 }
@@ -126,16 +107,16 @@ TS_DEV u32x2 read_vt4(const uint16_t (*sv)[128], uint32_t key, uint32_t d) {
 // block's K and V are loaded and staged once for all of them.
 template <bool QF32, int HG>
 __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
-    constexpr int kC = kKeys * 16 / (256 * HG);  // 16-byte K (and V) loads per thread and block
-    __shared__ __attribute__((aligned(16))) uint16_t sk[kKeys][128];     // K rows, swizzled chunks
-    __shared__ __attribute__((aligned(16))) uint16_t sv[kKeys][128];     // V rows, swizzled as K
+    constexpr int kWaves = 4 * HG;
+    constexpr int kNI = kKeys * 256 / 1024 / kWaves;  // 1 KiB K (and V) loads per wave and block
+    extern __shared__ __attribute__((aligned(16))) char kv_lds[];  // 2 x kBlockBytes
     __shared__ uint32_t srange[kRows][2];   // key range of each pass
     __shared__ uint32_t sslot[kRows];       // slot of each row; then the slot of each pass
     __shared__ uint32_t spass[kRows];       // pass of each row (kNoPass: dead or refused)
     __shared__ uint32_t snpass, smixed;
     __shared__ uint32_t stab_s[kMaxPages];  // this group's page-table entries
 
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, t = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), t = threadIdx.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
     const uint32_t G = p.heads / p.kv_heads, h = blockIdx.y * HG + (wave >> 2), kvh = h / G;
     const uint32_t qw = wave & 3;  // the wave's 16 kQT rows within the group's kRows
@@ -246,6 +227,14 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         }
     }
 
+    // LDS byte offsets of this lane's fragments within a block buffer: K as S^T's A
+    // operand (key 16 kt + col, d chunk 4 grp + j) and V^T as the A operand of P V
+    // (keys 32 st + 4 grp + col / 4 and + 16, d 16 d + 4 (col & 3)).
+    uint32_t koff[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) koff[j] = col * 256 + (((4 * grp + j) ^ col) << 4);
+    const uint32_t vk = 4 * grp + (col >> 2), vbase = vk * 256 + 8 * (col & 1), vc = (col & 3) >> 1;
+
     const float sl = p.scale * 1.4426950408889634f;  // scores to base 2
     float m[kQT], l[kQT];
 #pragma unroll
@@ -277,22 +266,29 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         __syncthreads();
         stab = stab_s;
     }
-    u32x4 kr[kC], vr[kC];
-    fetch_kv(p, slot, kvh, lo, hi, stab, p0, kr, vr);
-    for (uint32_t kb = lo; kb <= hi; kb += kKeys) {
-        // Every wave is done reading the previous block's K and V^T.
-        lds_barrier();
+    // Block kb's K and V rows straight into LDS buffer buf (global_load_lds: lane i of
+    // a wave's 1 KiB segment lands at 16 i, so the swizzle picks the source chunk).
+    // Keys past hi read row hi instead (written, finite; masked below).
+    auto fetch = [&](uint32_t kb, uint32_t buf) {
+        char *base = kv_lds + buf * kBlockBytes;
 #pragma unroll
-        for (int c = 0; c < kC; c++) {
-            const uint32_t idx = t + 256 * HG * c, key = idx >> 4, chunk = idx & 15;
-            *(u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8] = kr[c];
-            *(u32x4 *)&sv[key][(chunk ^ (key & 15)) * 8] = vr[c];
+        for (int c = 0; c < kNI; c++) {
+            const uint32_t sg = c * kWaves + wave, key = 4 * sg + (lane >> 4), chunk = (lane & 15) ^ (key & 15);
+            const uint64_t row = key_row(p, slot, min(kb + key, hi), stab, p0);
+            const size_t e = (row * p.kv_heads + kvh) * 128 + chunk * 8;
+            __builtin_amdgcn_global_load_lds((const void *)(p.k + e), (flash_lds_void *)(base + sg * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((const void *)(p.v + e),
+                                             (flash_lds_void *)(base + kKeys * 256 + sg * 1024), 16, 0, 0);
         }
-        // The next block's loads fly while this one computes (the barrier below
-        // waits for LDS only).
-        if (kb + kKeys <= hi) fetch_kv(p, slot, kvh, kb + kKeys, hi, stab, p0, kr, vr);
-        lds_barrier();
+    };
+    fetch(lo, 0);
+    for (uint32_t kb = lo, b = 0; kb <= hi; kb += kKeys, b++) {
+        // Block b has landed (its loads are the only ones outstanding); the barrier
+        // also ends every wave's reads of the buffer refilled next (block b - 1).
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kb + kKeys <= hi) fetch(kb + kKeys, (b + 1) & 1);
         if (!wave_on) continue;
+        const char *kbuf = kv_lds + (b & 1) * kBlockBytes, *vbuf = kbuf + kKeys * 256;
 
         // S^T for four 16-key tiles x the query tiles.
         f32x4 s[4][kQT];
@@ -300,11 +296,9 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         for (int kt = 0; kt < 4; kt++) {
 #pragma unroll
             for (int qt = 0; qt < kQT; qt++) s[kt][qt] = f32x4{0, 0, 0, 0};
-            const uint32_t key = kt * 16 + col;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t chunk = grp * 4 + j;  // d [32 grp + 8 j, +8): q's order
-                const bf16x8 kf = as_bf16x8(*(const u32x4 *)&sk[key][(chunk ^ (key & 15)) * 8]);
+                const bf16x8 kf = as_bf16x8(*(const u32x4 *)(kbuf + koff[j] + kt * 16 * 256));
 #pragma unroll
                 for (int qt = 0; qt < kQT; qt++) {
                     s[kt][qt] = mfma16(kf, as_bf16x8(qh[qt][j]), s[kt][qt]);
@@ -338,8 +332,12 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
                     mx = fmaxf(mx, sv[kt][i]);
                 }
             mx = rows4_max(mx);
-            const float mn = fmaxf(m[qt], mx);
-            const float alpha = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[qt] - mn);
+            // The reference point m moves only when a score passes it by more than
+            // kSlack (base 2): p = 2^(score - m) then stays below 2^kSlack, and most
+            // blocks leave l and O unscaled (O / l does not depend on the choice of m).
+            const bool raise = mx > m[qt] + kSlack;
+            const float mn = raise ? mx : m[qt];
+            const float alpha = raise ? __builtin_amdgcn_exp2f(m[qt] - mn) : 1.0f;  // 0 from m = -inf
             const float mo = mn == -INFINITY ? 0.0f : mn;  // exp2(-inf - 0) = 0 for masked keys
             float sum = 0.0f;
 #pragma unroll
@@ -354,8 +352,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
                         const float pb = __builtin_amdgcn_exp2f(sv[kt][i + 1] - mo);
                         sum += pa;
                         sum += pb;
-                        // p in [0, 1] (never NaN for finite scores): the plain
-                        // round-to-nearest-even conversion, no NaN fix-up.
+                        // p in [0, 2^kSlack] (never NaN for finite scores): the
+                        // plain round-to-nearest-even conversion, no NaN fix-up.
                         hw[2 * tt + i / 2] = __builtin_bit_cast(
                             uint32_t, __builtin_convertvector(ts_f32x2{pa, pb}, ts_bf16x2));
                         if (QF32) {
@@ -372,8 +370,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             sum = rows4_sum(sum);
             l[qt] = l[qt] * alpha + sum;
             m[qt] = mn;
-            // Rescale O only when some query of the wave has a new maximum.
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.0f) != 0) {
+            // Rescale O only when some query of the wave moved its reference point.
+            if (__builtin_amdgcn_ballot_w64(raise) != 0) {
 #pragma unroll
                 for (int d = 0; d < 8; d++) o[qt][d] *= alpha;
             }
@@ -386,8 +384,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             for (int st = 0; st < 2; st++) {
                 // Positions 8 grp .. + 3 and + 4 .. + 7 of step st hold keys
                 // 32 st + 4 grp + i and 32 st + 16 + 4 grp + i (P^T's order).
-                const uint32_t key = 32 * st + 4 * grp + (col >> 2), dd = d * 16 + 4 * (col & 3);
-                const u32x2 va = read_vt4(sv, key, dd), vb = read_vt4(sv, key + 16, dd);
+                const char *va_at = vbuf + vbase + (((2 * d + vc) ^ vk) << 4) + 32 * st * 256;
+                const u32x2 va = read_vt4(va_at), vb = read_vt4(va_at + 16 * 256);
                 const bf16x8 vf = as_bf16x8(u32x4{va.x, va.y, vb.x, vb.y});
 #pragma unroll
                 for (int qt = 0; qt < kQT; qt++) {
@@ -440,7 +438,17 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
     const bool f32 = a->q_dtype == TS_F32;
     const auto kern = hg == 2 ? (f32 ? flash_rows_kernel<true, 2> : flash_rows_kernel<false, 2>)
                               : (f32 ? flash_rows_kernel<true, 1> : flash_rows_kernel<false, 1>);
-    hipLaunchKernelGGL(kern, dim3((a->rows + kRows - 1) / kRows, a->heads / hg), dim3(256 * hg), 0,
+    static bool attr = false;
+    if (!attr) {  // the key blocks (dynamic) plus the static tables
+        for (const auto k : {flash_rows_kernel<true, 2>, flash_rows_kernel<false, 2>, flash_rows_kernel<true, 1>,
+                             flash_rows_kernel<false, 1>}) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     2 * kBlockBytes);
+            if (e != hipSuccess) return ts::hip_status(e, "flash_rows: shared memory attribute");
+        }
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((a->rows + kRows - 1) / kRows, a->heads / hg), dim3(256 * hg), 2 * kBlockBytes,
                        (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("flash_rows launch");
     return TS_OK;
