@@ -123,32 +123,43 @@ def copy_reference(torch, nbytes=256 << 20, reps=5):
 
 
 def gemm_sweep(torch, reps=10):
-    """C2 at M=2048: bf16 x and w, f32 accumulate, bf16 out; TFLOP/s per shape."""
+    """C2 at M=2048: bf16 x and w, f32 accumulate, bf16 out; TFLOP/s per shape.
+    Beside each shape, the vendor BLAS on the same operands and the same clock
+    (torch.mm, hipBLASLt on this image): a reference for what the part reaches on the
+    shape, not part of the measured path."""
     from tessera_amd import rules
     shapes = {"q": (1024, 2048), "kv": (1024, 1024), "o": (2048, 1024), "gate_up": (1024, 6144),
               "down": (3072, 1024), "lm_head": (1024, 151936)}
     M = 2048
-    res, flops_all, t_all = {}, 0.0, 0.0
-    for name, (K, N) in shapes.items():
-        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
-        w = torch.randn((N, K), device="cuda").to(torch.bfloat16)
-        out = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+
+    def clock(fn):
         for _ in range(2):
-            rules.tiled(x, w, out=out)
+            fn()
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         for _ in range(reps):
-            rules.tiled(x, w, out=out)
+            fn()
         e.record()
         torch.cuda.synchronize()
-        t = s.elapsed_time(e) / 1e3 / reps
+        return s.elapsed_time(e) / 1e3 / reps
+
+    res, flops_all, t_all, tv_all = {}, 0.0, 0.0, 0.0
+    for name, (K, N) in shapes.items():
+        x = torch.randn((M, K), device="cuda").to(torch.bfloat16)
+        w = torch.randn((N, K), device="cuda").to(torch.bfloat16)
+        out = torch.empty((M, N), device="cuda", dtype=torch.bfloat16)
+        t = clock(lambda: rules.tiled(x, w, out=out))
+        tv = clock(lambda: torch.mm(x, w.t(), out=out))
         fl = 2.0 * M * N * K
-        res[name] = {"us": round(t * 1e6, 2), "tflops": round(fl / t / 1e12, 1), "frac": round(fl / t / BF16_PEAK, 4)}
+        res[name] = {"us": round(t * 1e6, 2), "tflops": round(fl / t / 1e12, 1), "frac": round(fl / t / BF16_PEAK, 4),
+                     "vendor_us": round(tv * 1e6, 2), "vendor_frac": round(fl / tv / BF16_PEAK, 4)}
         flops_all += fl
         t_all += t
+        tv_all += tv
         del x, w, out
-    return {"M": M, "shapes": res, "aggregate_frac": round(flops_all / t_all / BF16_PEAK, 4)}
+    return {"M": M, "shapes": res, "aggregate_frac": round(flops_all / t_all / BF16_PEAK, 4),
+            "vendor_aggregate_frac": round(flops_all / tv_all / BF16_PEAK, 4), "vendor": "torch.mm (hipBLASLt)"}
 
 
 def _graph_time(torch, fn, launches=20, replays=5):
@@ -220,8 +231,33 @@ def c3_prefill(torch):
                                   kept_pages=kept_pages, page=page, max_position=n - 1, out=out)
     t = _graph_time(torch, fn, launches=5)
     flops = seqs * heads * (n * (n + 1) // 2) * 4 * width
-    return {"bound": "mfma", "us": round(t * 1e6, 2), "tflops": round(flops / t / 1e12, 1),
-            "frac": round(flops / t / BF16_PEAK, 4), "gflop": round(flops / 1e9, 2)}
+    res = {"bound": "mfma", "us": round(t * 1e6, 2), "tflops": round(flops / t / 1e12, 1),
+           "frac": round(flops / t / BF16_PEAK, 4), "gflop": round(flops / 1e9, 2)}
+    # Reference: torch's fused attention on the same sizes with dense (unpaged) K/V,
+    # bf16 out (its flash backend on this image), not part of the measured path.
+    del k, v, q, out
+    try:
+        import torch.nn.functional as F
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        qd = torch.randn((seqs, heads, n, width), device="cuda", dtype=torch.bfloat16)
+        kd = torch.randn((seqs, kvh, n, width), device="cuda", dtype=torch.bfloat16)
+        vd = torch.randn((seqs, kvh, n, width), device="cuda", dtype=torch.bfloat16)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            run = lambda: F.scaled_dot_product_attention(qd, kd, vd, is_causal=True, enable_gqa=True)
+            run()
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(10):
+                run()
+            e.record()
+            torch.cuda.synchronize()
+            tv = s.elapsed_time(e) / 1e3 / 10
+        res.update({"vendor_us": round(tv * 1e6, 2), "vendor_frac": round(flops / tv / BF16_PEAK, 4),
+                    "vendor": "torch scaled_dot_product_attention (flash backend, dense K/V)"})
+    except Exception as e:  # the reference is optional: report why it is missing
+        res["vendor"] = f"unavailable: {type(e).__name__}"
+    return res
 
 
 def c4(torch):
