@@ -176,16 +176,23 @@ TS_DEV bool spin(Ctx &c, uint32_t &it, uint64_t &t0) {
     return true;
 }
 
-// Tagged words src[tid + kT k] (k < NX, index < n) into v[k], and (extra non-null)
-// one more word into *xv: every load is issued, then the loads whose epoch is stale
-// are reissued until none is.
+// The words a thread takes of an input vector: base + stride k, k < NX. Group-wide
+// (base tid, stride kT) or one wave's own range (base 32 KS wave + lane, stride 64).
+struct Words {
+    uint32_t base, stride;
+};
+TS_DEV Words group_words(const Ctx &c) { return {c.tid, kT}; }
+
+// Tagged words src[w.base + w.stride k] (k < NX, index < n) into v[k], and (extra
+// non-null) one more word into *xv: every load is issued, then the loads whose epoch
+// is stale are reissued until none is.
 template <int NX>
-TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[NX],
+TS_DEV void poll(Ctx &c, Words ws, const uint64_t *src, uint32_t n, uint32_t tag, float (&v)[NX],
                  const uint64_t *extra = nullptr, float *xv = nullptr) {
     uint64_t w[NX], x;
 #pragma unroll
     for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kT * k;
+        const uint32_t i = ws.base + ws.stride * k;
         w[k] = i < n ? ld_tag(src + i) : ((uint64_t)tag << 32);
     }
     x = extra ? ld_tag(extra) : ((uint64_t)tag << 32);
@@ -198,7 +205,7 @@ TS_DEV void poll(Ctx &c, const uint64_t *src, uint32_t n, uint32_t tag, float (&
         if (ready || !spin(c, it, t0)) break;
 #pragma unroll
         for (int k = 0; k < NX; k++)
-            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(src + c.tid + kT * k);
+            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_tag(src + ws.base + ws.stride * k);
         if ((uint32_t)(x >> 32) != tag) x = ld_tag(extra);
     }
 #pragma unroll
@@ -226,10 +233,10 @@ TS_DEV void await(Ctx &c, const uint64_t *src, uint32_t tag) {
 
 // Gains of the words this thread stages (1 without a gain), loaded before the poll.
 template <int NX>
-TS_DEV void gains(const Ctx &c, const float *g, uint32_t n, float (&gv)[NX]) {
+TS_DEV void gains(const Ctx &c, Words ws, const float *g, uint32_t n, float (&gv)[NX]) {
 #pragma unroll
     for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kT * k;
+        const uint32_t i = ws.base + ws.stride * k;
         gv[k] = g && i < n ? g[i] : 1.0f;
     }
 }
@@ -239,12 +246,12 @@ TS_DEV void gains(const Ctx &c, const float *g, uint32_t n, float (&gv)[NX]) {
 // operand columns of the matrix-unit products; and the group's partial sums of
 // squares of v (read after the next barrier by norm_inv).
 template <int NX>
-TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX]) {
+TS_DEV void stage(Ctx &c, Words ws, const float (&v)[NX], uint32_t n, const float (&g)[NX]) {
     float ss = 0.0f;
     uint16_t *xs = c.xs();
 #pragma unroll
     for (int k = 0; k < NX; k++) {
-        const uint32_t i = c.tid + kT * k;
+        const uint32_t i = ws.base + ws.stride * k;
         if (i < n) {
             const float x = v[k] * g[k];
             const uint16_t hi = bf16_bits(x);
@@ -262,9 +269,9 @@ TS_DEV void stage(Ctx &c, const float (&v)[NX], uint32_t n, const float (&g)[NX]
 
 // 1/sqrt(mean(v^2) + eps): the RmsNorm scale, folded into the products' results
 // (sum_k (x_k inv g_k) w_k = inv sum_k (x_k g_k) w_k).
-TS_DEV float norm_inv(const Ctx &c, uint32_t n, float eps) {
+TS_DEV float norm_inv(const float *ssq, uint32_t n, float eps) {
     float t = 0.0f;
-    for (uint32_t w = 0; w < kW; w++) t += c.ssq()[w];
+    for (uint32_t w = 0; w < kW; w++) t += ssq[w];
     return 1.0f / sqrtf(t / (float)n + eps);
 }
 
@@ -349,15 +356,15 @@ TS_DEV void lm_rows(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t,
     if (tiles > 2) load(2, a2);
     {
         float v[2], gv[2];
-        gains<2>(c, p.norm, H, gv);
+        gains<2>(c, group_words(c), p.norm, H, gv);
         const uint64_t *blk = p.hand + (size_t)(p.L - 1) * hd.block;
         await(c, blk + hd.hf + c.wave * (p.F / kW), tag);  // the last gate/up first
-        poll<2>(c, blk + hd.xo, H, tag, v);
-        stage<2>(c, v, H, gv);
+        poll<2>(c, group_words(c), blk + hd.xo, H, tag, v);
+        stage<2>(c, group_words(c), v, H, gv);
     }
     mark(p, c, t, p.L, 0);
     bar();
-    const float inv = norm_inv(c, H, p.eps);
+    const float inv = norm_inv(c.ssq(), H, p.eps);
     const uint16_t *xs = c.xs();
     c.ph++;
     u32x4 xb[KS];
@@ -459,11 +466,12 @@ TS_DEV uint32_t pick(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t t
 // Product roles. The group's outputs [s.first, s.first + s.count) of one matrix, as
 // TILES 16-row tiles (gate/up: TILES / 2 gate tiles, then the matching up tiles),
 // held in registers: wave w keeps k-steps [KS w, KS w + KS) of every tile. Per
-// layer: poll the input (the RmsNorm gains loaded first; o and down also poll their
-// residual rows), stage it, one barrier, the MFMAs, the partials to LDS, a barrier,
-// each output summed over the waves by one thread and published by consecutive
-// threads (whole lines per store instruction); then the next layer's tiles are
-// loaded into the same registers.
+// layer: each wave polls the input words of its own k-steps (the RmsNorm gains loaded
+// first; o and down also poll their residual rows), stages them, and runs its MFMAs
+// without waiting for the other waves; the partials go to LDS, one barrier, each
+// output is summed over the waves by one thread (with the RmsNorm scale from the
+// waves' sums of squares) and published by consecutive threads (whole lines per
+// store instruction); then the next layer's tiles are loaded into the same registers.
 // ---------------------------------------------------------------------------
 template <uint32_t KIND, int TILES, int KS, int NX>
 TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32_t idx, uint32_t count) {
@@ -472,6 +480,8 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
     const uint32_t K = KIND == kQkv || KIND == kGu ? H : (KIND == kO ? QD : F);
     const Split s = split(N, count, idx);
     constexpr int OT = KIND == kGu ? TILES / 2 : TILES;  // tiles of outputs
+    static_assert(NX * 64 == KS * 32, "a wave polls exactly the words of its k-steps");
+    const Words ws = {32 * KS * c.wave + c.lane, 64};  // this wave's input words
     u32x4 w[TILES][KS];
     // The packed tiles (decode_step_pack): tile t, k-step ks of this group is 1 KB at
     // ((idx * TILES + t) * KSt + ks) KiB, lane l's 16 bytes at l * 16.
@@ -502,7 +512,7 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
             // rows (one word a thread, polled with the input).
             float v[NX], gv[NX];
             const uint32_t n = K;
-            gains<NX>(c, KIND == kQkv ? p.ln1[l] : (KIND == kGu ? p.ln2[l] : nullptr), n, gv);
+            gains<NX>(c, ws, KIND == kQkv ? p.ln1[l] : (KIND == kGu ? p.ln2[l] : nullptr), n, gv);
             const bool has_res = (KIND == kO || KIND == kDn) && c.tid < s.count;
             const uint64_t *res_src = nullptr;
             float rv = 0.0f;
@@ -517,7 +527,7 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
             if (KIND == kQkv && !prev) {
 #pragma unroll
                 for (int k = 0; k < NX; k++) {
-                    const uint32_t i = c.tid + kT * k;
+                    const uint32_t i = ws.base + ws.stride * k;
                     v[k] = i < n ? bf16_float(p.embed[(size_t)tok * H + i]) : 0.0f;
                 }
             } else {
@@ -531,15 +541,17 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
                     const uint32_t pn = KIND == kQkv ? F : (KIND == kO ? QKV : (KIND == kGu ? QD : H));
                     await(c, pre + c.wave * (pn / kW), tag);
                 }
-                poll<NX>(c, in, n, tag, v, res_src, &rv);
+                poll<NX>(c, ws, in, n, tag, v, res_src, &rv);
             }
             if (has_res) c.res()[c.tid] = rv;
-            stage<NX>(c, v, n, gv);
+            stage<NX>(c, ws, v, n, gv);
             mark(p, c, t, l, 0);
-            bar();
-            const float inv = KIND == kQkv || KIND == kGu ? norm_inv(c, n, p.eps) : 1.0f;
+            // No barrier: a wave's fragments come from the words it staged itself
+            // (LDS operations of one wave complete in order), so each wave starts its
+            // MFMAs once its own words are in; the residual words and the sums of
+            // squares are read after the barrier that ends the products.
             const uint16_t *xs = c.xs();
-            const float *res = c.res();
+            const float *res = c.res(), *ssq = c.ssq();
             c.ph++;
             if (s.count) {
 #ifdef TS_FINE
@@ -584,6 +596,7 @@ TS_DEV void product_role(const DecodeStepArgs &p, Ctx &c, const Hand &hd, uint32
                     float x = 0.0f;
 #pragma unroll
                     for (uint32_t w2 = 0; w2 < kW; w2++) x += part[w2 * 64 + o];
+                    const float inv = KIND == kQkv || KIND == kGu ? norm_inv(ssq, n, p.eps) : 1.0f;
                     float y;
                     if (KIND == kQkv) {
                         y = x * inv;
