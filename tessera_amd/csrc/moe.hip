@@ -110,6 +110,99 @@ __global__ __launch_bounds__(kScan) void route_scan(uint32_t *offs, uint32_t chu
     }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+TS_DEV uint32_t wave_scan(uint32_t v, uint32_t lane) {
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
+// route_scan for up to kFastChunks chunks and kFastBuckets buckets, one coalesced
+// load and one coalesced store of the counts: wave w takes chunks [kFastCW w, +kFastCW)
+// with lane l on buckets l, l + 64, ... (the [chunk][bucket] layout's contiguous
+// direction); the waves' sums per bucket are scanned over the waves in LDS, one
+// wave scans the bucket totals and row tiles, and every wave stores absolute
+// positions.
+constexpr uint32_t kFastWaves = kScan / 64, kFastCW = 8, kFastBS = 5;
+constexpr uint32_t kFastChunks = kFastWaves * kFastCW, kFastBuckets = 64 * kFastBS;
+__global__ __launch_bounds__(kScan) void route_scan_fast(uint32_t *offs, uint32_t chunks, uint32_t rows,
+                                                         uint32_t count, uint32_t tile_rows, uint32_t *row_start,
+                                                         uint32_t *tile_start) {
+    __shared__ uint32_t wsum[kFastWaves][kFastBuckets], tot_s[kFastBuckets], base_s[kFastBuckets];
+    const uint32_t B = count + 1, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t v[kFastBS][kFastCW];
+#pragma unroll
+    for (uint32_t j = 0; j < kFastBS; j++) {
+        const uint32_t b = 64 * j + lane;
+#pragma unroll
+        for (uint32_t i = 0; i < kFastCW; i++) {
+            const uint32_t c = kFastCW * wave + i;
+            v[j][i] = b < B && c < chunks ? offs[(size_t)c * B + b] : 0u;
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kFastBS; j++) {
+        uint32_t sum = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < kFastCW; i++) sum += v[j][i];
+        wsum[wave][64 * j + lane] = sum;
+    }
+    __syncthreads();
+    if (threadIdx.x < B) {  // one thread a bucket: the waves' sums, exclusive, in wave order
+        const uint32_t b = threadIdx.x;
+        uint32_t run = 0;
+        for (uint32_t w = 0; w < kFastWaves; w++) {
+            const uint32_t x = wsum[w][b];
+            wsum[w][b] = run;
+            run += x;
+        }
+        tot_s[b] = run;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        constexpr uint32_t kPer = kFastBS;  // consecutive buckets a lane
+        uint32_t rs = 0, ts = 0;
+        for (uint32_t i = 0; i < kPer; i++) {
+            const uint32_t b = lane * kPer + i;
+            if (b < B) {
+                rs += tot_s[b];
+                ts += b < count ? (tot_s[b] + tile_rows - 1) / tile_rows : 0;
+            }
+        }
+        uint32_t rb = wave_scan(rs, lane) - rs, tb = wave_scan(ts, lane) - ts;
+        for (uint32_t i = 0; i < kPer; i++) {
+            const uint32_t b = lane * kPer + i;
+            if (b < B) {
+                base_s[b] = rb;
+                row_start[b] = rb;
+                if (b < count) tile_start[b] = tb;
+                rb += tot_s[b];
+                tb += b < count ? (tot_s[b] + tile_rows - 1) / tile_rows : 0;
+            }
+        }
+        if (lane == 63) {
+            row_start[B] = rows;
+            tile_start[count] = tb;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (uint32_t j = 0; j < kFastBS; j++) {
+        const uint32_t b = 64 * j + lane;
+        if (b >= B) continue;
+        uint32_t at = base_s[b] + wsum[wave][b];
+#pragma unroll
+        for (uint32_t i = 0; i < kFastCW; i++) {
+            const uint32_t c = kFastCW * wave + i;
+            if (c < chunks) offs[(size_t)c * B + b] = at;
+            at += v[j][i];
+        }
+    }
+}
+
 // Stable placement: a row's position is its chunk's first position in its bucket
 // plus the rows of the same bucket before it in the chunk.
 __global__ __launch_bounds__(kChunk) void route_place(const uint32_t *ids, uint32_t rows, uint32_t first,
@@ -168,6 +261,36 @@ __global__ __launch_bounds__(256) void softmax_kernel(const float *x, float *out
 
 // mix / weighted mean (cpu.rs:450-473): out[o, i] = sum_t x[o, t, i] * w[o, t], in t
 // order from 0, each product rounded before the add (no fused multiply-add).
+// Four adjacent columns a thread (16-byte loads, every pick's load issued before the
+// adds) when inner is a multiple of 4 and the buffers 16-byte aligned.
+__global__ __launch_bounds__(256) void mix4_kernel(const float *x, const float *w, float *out, uint32_t outer,
+                                                   uint32_t count, uint32_t inner) {
+#pragma clang fp contract(off)  // the reference rounds each product before the add
+    const uint32_t q = inner / 4;
+    const uint64_t j = blockIdx.x * 256ull + threadIdx.x;
+    if (j >= (uint64_t)outer * q) return;
+    const uint32_t o = (uint32_t)(j / q), i = (uint32_t)(j % q) * 4;
+    const float even = 1.0f / (float)count;
+    float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    constexpr uint32_t kB = 8;  // picks in flight
+    for (uint32_t t0 = 0; t0 < count; t0 += kB) {
+        float4 v[kB];
+#pragma unroll
+        for (uint32_t u = 0; u < kB; u++)
+            if (t0 + u < count) v[u] = *(const float4 *)(x + ((size_t)o * count + t0 + u) * inner + i);
+#pragma unroll
+        for (uint32_t u = 0; u < kB; u++)
+            if (t0 + u < count) {
+                const float wt = w ? w[(size_t)o * count + t0 + u] : even;
+                s.x = s.x + v[u].x * wt;
+                s.y = s.y + v[u].y * wt;
+                s.z = s.z + v[u].z * wt;
+                s.w = s.w + v[u].w * wt;
+            }
+    }
+    *(float4 *)(out + (size_t)o * inner + i) = s;
+}
+
 __global__ __launch_bounds__(256) void mix_kernel(const float *x, const float *w, float *out, uint32_t outer,
                                                   uint32_t count, uint32_t inner) {
 #pragma clang fp contract(off)  // the reference rounds each product before the add
@@ -201,8 +324,12 @@ int route_launch(const uint32_t *ids, uint32_t rows, uint32_t first, uint32_t co
     const hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(route_count, dim3(chunks), dim3(kChunk), B * sizeof(uint32_t), s, ids, rows, first, count,
                        offs);
-    hipLaunchKernelGGL(route_scan, dim3(1), dim3(kScan), 0, s, offs, chunks, rows, count, tile_rows,
-                       route->row_start, route->tile_start);
+    if (chunks <= kFastChunks && B <= kFastBuckets)
+        hipLaunchKernelGGL(route_scan_fast, dim3(1), dim3(kScan), 0, s, offs, chunks, rows, count, tile_rows,
+                           route->row_start, route->tile_start);
+    else
+        hipLaunchKernelGGL(route_scan, dim3(1), dim3(kScan), 0, s, offs, chunks, rows, count, tile_rows,
+                           route->row_start, route->tile_start);
     hipLaunchKernelGGL(route_place, dim3(chunks), dim3(kChunk), 0, s, ids, rows, first, count, offs, route->perm);
     TS_CHECK_LAUNCH("picked routing");
     return TS_OK;
@@ -256,8 +383,14 @@ extern "C" int tessera_hip_mix(const ts_mix_args *a, void *stream) {
     TS_REQUIRE(count >= 1, "mix: count 0");
     const uint64_t total = (uint64_t)outer * inner;
     if (total == 0) return TS_OK;
-    hipLaunchKernelGGL(ts::mix_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, x,
-                       weights, out, outer, count, inner);
+    if (inner % 4 == 0 && ts::aligned(x, 16) && ts::aligned(out, 16)) {
+        const uint64_t quads = total / 4;
+        hipLaunchKernelGGL(ts::mix4_kernel, dim3((uint32_t)((quads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                           x, weights, out, outer, count, inner);
+    } else {
+        hipLaunchKernelGGL(ts::mix_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                           x, weights, out, outer, count, inner);
+    }
     TS_CHECK_LAUNCH("mix launch");
     return TS_OK;
 }

@@ -48,6 +48,7 @@ def _picked_want(x, table_bits, ids, repeat, first, offset, n, silu):
     (300, 16, 256, 96, 1, 0, "f32"),
     (600, 16, 128, 130, 4, 2, "bf16"),   # ids below `first` and past the set read zeros
     (2000, 64, 64, 64, 8, 0, "bf16"),
+    (1000, 330, 64, 32, 1, 0, "bf16"),  # more matrices than the one-pass routing scan takes
 ])
 def test_picked_matches_oracle(rows, count, k, n, repeat, first, xdt):
     R = _rules()
@@ -73,6 +74,22 @@ def test_picked_matches_oracle(rows, count, k, n, repeat, first, xdt):
         else:
             b = _bound(xs[i:i + 1], table[e, offset:offset + n])[0]
             assert np.all(np.abs(got[i] - want[i]) <= b), f"row {i} expert {e}"
+
+
+def test_picked_many_rows():
+    """Past 32768 rows the routing scan takes its general path; every row within its
+    matrix's bound, in one vectorized check per matrix."""
+    R = _rules()
+    r = rng(41)
+    rows, count, k, n = 40000, 3, 64, 16
+    table_bits, table = bf16_bits_normal(r, (count, n, k), 0.05)
+    xb, x = bf16_bits_normal(r, (rows, k))
+    ids = r.integers(0, count, size=rows).astype(np.uint32)
+    want = O.product_picked_bf16w(x, table_bits, ids, 0)
+    got = from_dev(R.picked(to_dev(xb, torch), to_dev(table_bits, torch), to_dev(ids.astype(np.int32), torch)))
+    for e in range(count):
+        sel = ids == e
+        assert np.all(np.abs(got[sel] - want[sel]) <= _bound(x[sel], table[e])), f"matrix {e}"
 
 
 def test_picked_silu_pair_bf16_out():
@@ -122,6 +139,8 @@ def test_take_softmax_mix():
     w = O.softmax(g)
     assert np.array_equal(from_dev(R.mix(to_dev(y, torch), to_dev(w, torch))), O.mix(y, w))
     assert np.array_equal(from_dev(R.mix(to_dev(y, torch))), O.mix(y))
+    y5 = r.standard_normal((rows, picks, 5)).astype(np.float32)  # inner not a multiple of 4
+    assert np.array_equal(from_dev(R.mix(to_dev(y5, torch), to_dev(w, torch))), O.mix(y5, w))
     # cpu_test.rs:161 softmax_rows
     rows2 = np.array([[1, 2, 3, 4], [0, 0, -np.inf, 0]], np.float32)
     want2 = np.array([[0.0320586, 0.0871443, 0.2368828, 0.6439143], [1 / 3, 1 / 3, 0, 1 / 3]], np.float32)
