@@ -446,6 +446,9 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         for (int j = 0; j < P::FJ; j++) acc[i][j] = f32x4{0, 0, 0, 0};
 
     const uint32_t steps = p.k / KD;
+    // 16-row fragments of this wave that hold a row of the tile (wave-uniform).
+    const uint32_t wrow0 = m0 + wm * P::WM;
+    const uint32_t live_frags = mend > wrow0 ? min((mend - wrow0 + 15) / 16, (uint32_t)P::FI) : 0u;
 #pragma unroll
     for (int s = 0; s < NS - 1; s++)
         if ((uint32_t)s < steps) fetch(s, s * KD);
@@ -455,19 +458,29 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         pipe_wait_ahead<P::NA + P::NB, NS - 2>(min(steps - 1 - s, (uint32_t)NS - 2));
         if (s + NS - 1 < steps) fetch((s + NS - 1) % NS, (s + NS - 1) * KD);
         const char *sa = lds + (s % NS) * P::STAGE, *sb = sa + P::A_BYTES;
+        // PICK mode: row fragments wholly past the matrix's last row (its partial last
+        // tile) skip their MFMAs; their loads and the barriers stay, so every wave keeps
+        // the same pipeline.
+        auto step = [&](const bool all) {
 #pragma unroll
-        for (int ks = 0; ks < KD / 32; ks++) {
-            const uint32_t chunk = ks * 4 + grp;
-            bf16x8 af[P::FI], bfr[P::FJ];
+            for (int ks = 0; ks < KD / 32; ks++) {
+                const uint32_t chunk = ks * 4 + grp;
+                bf16x8 af[P::FI], bfr[P::FJ];
 #pragma unroll
-            for (int i = 0; i < P::FI; i++) af[i] = as_bf16x8(*(const u32x4 *)(sa + P::at(wm * P::WM + i * 16 + col, chunk)));
+                for (int i = 0; i < P::FI; i++)
+                    if (all || (uint32_t)i < live_frags)
+                        af[i] = as_bf16x8(*(const u32x4 *)(sa + P::at(wm * P::WM + i * 16 + col, chunk)));
 #pragma unroll
-            for (int j = 0; j < P::FJ; j++) bfr[j] = as_bf16x8(*(const u32x4 *)(sb + P::at(wn * P::WN + j * 16 + col, chunk)));
+                for (int j = 0; j < P::FJ; j++) bfr[j] = as_bf16x8(*(const u32x4 *)(sb + P::at(wn * P::WN + j * 16 + col, chunk)));
 #pragma unroll
-            for (int i = 0; i < P::FI; i++)
+                for (int i = 0; i < P::FI; i++)
+                    if (all || (uint32_t)i < live_frags)
 #pragma unroll
-                for (int j = 0; j < P::FJ; j++) acc[i][j] = mfma16(bfr[j], af[i], acc[i][j]);
-        }
+                        for (int j = 0; j < P::FJ; j++) acc[i][j] = mfma16(bfr[j], af[i], acc[i][j]);
+            }
+        };
+        if (!PICK || live_frags >= (uint32_t)P::FI) step(true);
+        else step(false);
     }
 
     // Epilogue. acc[i][j] is the transposed 16x16 tile: lane (col, grp) holds tile row
