@@ -15,7 +15,8 @@
 //    block is one table lookup). Scores S[16 heads, 16 keys] come from four
 //    v_mfma_f32_16x16x32_bf16 steps per q part: each lane loads 64 contiguous
 //    bytes of one key row (B operand), q is split into two bf16 parts.
-//  * Online softmax per head in registers (16-lane butterflies), then P*V on
+//  * Online softmax per head in registers (16-lane butterflies, base 2 on
+//    v_exp_f32), then P*V on
 //    the vector ALUs: a lane owns 2 adjacent head dims, so each V row is one
 //    256-byte coalesced load across the wave.
 //  * A group's waves (up to 8) split its keys and merge (max, sum, acc) in LDS.
@@ -50,6 +51,9 @@ extern "C" int tessera_hip_debug_marks(uint64_t *host, uint32_t count) {
 namespace {
 
 constexpr int kMaxWaves = 8;  // 512 threads: room for two blocks of K/V in registers
+// Softmax in base 2: scores times scale log2(e), exponentials on v_exp_f32 (2^x), so
+// every running maximum and partial's maximum (and the merges) are base 2.
+constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxG = 16;
 
 struct RowsParams {
@@ -279,10 +283,10 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         float alpha[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float si = valid ? s[i] * p.scale : -INFINITY;
+            const float si = valid ? s[i] * (p.scale * kLog2e) : -INFINITY;  // base 2
             const float mn = fmaxf(m[i], row16_max(si));
-            alpha[i] = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
-            const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
+            alpha[i] = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
+            const float pi = (mn == -INFINITY || !valid) ? 0.0f : __builtin_amdgcn_exp2f(si - mn);
             l[i] = l[i] * alpha[i] + row16_sum(pi);
             m[i] = mn;
             const uint32_t h = 4 * grp + i;
@@ -354,7 +358,7 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
         for (uint32_t w = 0; w < waves; w++) M = fmaxf(M, sm[w][h]);
         float L = 0.0f, O = 0.0f;
         for (uint32_t w = 0; w < waves; w++) {
-            const float f = (sm[w][h] == -INFINITY) ? 0.0f : expf(sm[w][h] - M);
+            const float f = (sm[w][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sm[w][h] - M);
             L += sl[w][h] * f;
             O += so[w][h][d] * f;
         }
@@ -496,10 +500,10 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
         float alpha[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float si = valid ? sc[i] * p.scale : -INFINITY;
+            const float si = valid ? sc[i] * (p.scale * kLog2e) : -INFINITY;  // base 2
             const float mn = fmaxf(m[i], row16_max(si));
-            alpha[i] = (mn == -INFINITY) ? 1.0f : expf(m[i] - mn);
-            const float pi = (mn == -INFINITY || !valid) ? 0.0f : expf(si - mn);
+            alpha[i] = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
+            const float pi = (mn == -INFINITY || !valid) ? 0.0f : __builtin_amdgcn_exp2f(si - mn);
             l[i] = l[i] * alpha[i] + row16_sum(pi);
             m[i] = mn;
             const uint32_t h = 4 * grp + i;
@@ -581,7 +585,7 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
         for (uint32_t w = 0; w < kLongWaves; w++) M = fmaxf(M, sm[w][h]);
         float L = 0.0f, O = 0.0f;
         for (uint32_t w = 0; w < kLongWaves; w++) {
-            const float f = (sm[w][h] == -INFINITY) ? 0.0f : expf(sm[w][h] - M);
+            const float f = (sm[w][h] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(sm[w][h] - M);
             L += sl[w][h] * f;
             O += so[w][h][d] * f;
         }
@@ -623,7 +627,7 @@ __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t 
 #pragma unroll
             for (uint32_t j = 0; j < kB; j++)
                 if (q0 + j < parts) {
-                    const float f = (mq[j] == -INFINITY) ? 0.0f : expf(mq[j] - M);
+                    const float f = (mq[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mq[j] - M);
                     L += lq[j] * f;
                     O += oq[j] * f;
                 }
