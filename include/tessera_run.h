@@ -62,6 +62,12 @@ int tessera_qwen3_prefill(ts_qwen3 *m, const uint32_t *tokens, uint32_t count, u
  * tokens_out (host) when it is not NULL. Synchronizes before returning. */
 int tessera_qwen3_decode(ts_qwen3 *m, uint32_t steps, uint32_t *tokens_out);
 
+/* Replaces the next decode step's input token (by default the previous step's greedy
+ * pick) with `token`: teacher forcing, as when a caller feeds its own sequence. The
+ * reference's decode loop feeds back its pick (engine/engine/src/lib.rs:401-470); this
+ * lets a caller, and the tests, drive the same step with any token. */
+int tessera_qwen3_set_token(ts_qwen3 *m, uint32_t token);
+
 /* The last step's logits (f32, vocab entries) copied to host. */
 int tessera_qwen3_logits(ts_qwen3 *m, float *host, uint64_t count);
 

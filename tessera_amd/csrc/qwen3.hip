@@ -79,6 +79,12 @@ __global__ void start_kernel(uint64_t *key, uint32_t *tok, uint32_t *pos, uint32
     hist[count] = take_token(key, tok, vocab);
 }
 
+// The next step's input token set from the host (teacher forcing), recorded at its position.
+__global__ void set_token_kernel(uint32_t *tok, uint32_t *hist, uint32_t at, uint32_t t) {
+    tok[0] = t;
+    hist[at] = t;
+}
+
 struct Layer {
     float *ln1, *q_norm, *k_norm, *ln2;
     uint16_t *qkv, *o, *gate_up, *down;
@@ -610,6 +616,15 @@ extern "C" int tessera_qwen3_logits(ts_qwen3 *m, float *host, uint64_t count) {
     hipError_t e = hipMemcpyAsync(host, m->logits, count * 4, hipMemcpyDeviceToHost, m->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
     if (e != hipSuccess) return ts::hip_status(e, "logits download");
+    return TS_OK;
+}
+
+extern "C" int tessera_qwen3_set_token(ts_qwen3 *m, uint32_t token) {
+    TS_REQUIRE(m && m->have_run, "qwen3_set_token: prefill first");
+    TS_REQUIRE(token < m->c.vocab, "qwen3_set_token: token %u past the vocabulary (%u)", token, m->c.vocab);
+    TS_REQUIRE(m->position <= m->c.max_context, "qwen3_set_token: context full");
+    hipLaunchKernelGGL(set_token_kernel, dim3(1), dim3(1), 0, m->stream, m->d_tok, m->d_hist, m->position, token);
+    TS_CHECK_LAUNCH("qwen3_set_token launch");
     return TS_OK;
 }
 

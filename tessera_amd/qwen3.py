@@ -30,6 +30,7 @@ SIGNATURES = {
     "tessera_qwen3_prefill": (C.c_int, [_P, _P, C.c_uint32, C.POINTER(C.c_uint32)]),
     "tessera_qwen3_decode": (C.c_int, [_P, C.c_uint32, _P]),
     "tessera_qwen3_logits": (C.c_int, [_P, _P, C.c_uint64]),
+    "tessera_qwen3_set_token": (C.c_int, [_P, C.c_uint32]),
     "tessera_qwen3_set_graph": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_set_step": (C.c_int, [_P, C.c_int]),
     "tessera_qwen3_step_mode": (C.c_int, [_P]),
@@ -105,6 +106,10 @@ class Qwen3:
         abi.check(self.L.tessera_qwen3_decode(self.h, steps, out.ctypes.data if want_tokens else None),
                   "tessera_qwen3_decode")
         return out
+
+    def set_token(self, token: int):
+        """The next decode step reads `token` instead of the previous greedy pick."""
+        abi.check(self.L.tessera_qwen3_set_token(self.h, int(token)), "tessera_qwen3_set_token")
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.config.vocab, np.float32)

@@ -112,3 +112,32 @@ def test_qwen3_c1_matches_oracle():
     prompt = np.random.default_rng(1).integers(0, 151936, 128).astype(np.uint32)
     toks = run_case(default_config(), 0, prompt, 32, 0.999, 2e-2)
     assert len(toks) == 33
+
+
+@pytest.mark.parametrize("step", [True, False], ids=["persistent", "graph"])
+def test_qwen3_c1_teacher_forced(step):
+    """C1 shape with the input tokens set from the host (random ids): every decode
+    step's logits against the oracle's forward over the same tokens, so positions
+    past the prompt see distinct embedding rows (greedy decode of random weights
+    repeats one token)."""
+    from tessera_amd.qwen3 import Qwen3, default_config
+    O.set_threads(O.lib().or_threads_available())
+    cfg = default_config()
+    r = np.random.default_rng(3)
+    prompt = r.integers(0, cfg.vocab, 64).astype(np.uint32)
+    forced = r.integers(0, cfg.vocab, 10).astype(np.uint32)
+    m = Qwen3(cfg, seed=0)
+    m.set_step(step)
+    ref = OracleQwen3(host_weights(m))
+    m.prefill(prompt)
+    ref.forward(prompt, np.arange(len(prompt)))
+    for i, t in enumerate(forced):
+        m.set_token(int(t))
+        m.decode(1)
+        got = m.logits()
+        want = ref.forward([int(t)], [len(prompt) + i])
+        c, rel = cosine(got, want), max_rel(got, want)
+        assert c >= 0.999 and rel <= 2e-2, (i, c, rel)
+    with pytest.raises(Exception, match="past the vocabulary"):
+        m.set_token(cfg.vocab)
+    m.close()
