@@ -67,6 +67,15 @@ def test_decode_rows_c3_sample():
     np.testing.assert_allclose(run("attend", c, s), want(c, s), atol=ATOL, rtol=0)
 
 
+def test_decode_rows_c3_full():
+    """The whole C3 decode shape: 32 rows, contexts U[512, 8192] (seed 2, as the bench
+    draws them), 16 q / 8 kv heads, shuffled 16-row pages."""
+    ctxs = rng(2).integers(512, 8193, 32).tolist()
+    c = paged_case(2, ctxs)
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("attend", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (32, 8), (16, 1)])
 def test_decode_gqa_groups(heads, kv_heads):
     c = paged_case(9 + heads, [300, 70], heads=heads, kv_heads=kv_heads)

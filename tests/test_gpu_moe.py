@@ -147,11 +147,12 @@ def test_take_softmax_mix():
     assert np.allclose(from_dev(R.softmax(to_dev(rows2, torch))), want2, atol=1e-6)
 
 
-def test_moe_layer_matches_oracle():
-    """One MoE MLP (decoder.rs:73-84) plus a shared expert, small shape."""
+@pytest.mark.parametrize("tokens,hidden,experts,top,ffn", [(384, 256, 16, 4, 128), (1024, 1024, 128, 8, 512)])
+def test_moe_layer_matches_oracle(tokens, hidden, experts, top, ffn):
+    """One MoE MLP (decoder.rs:73-84) plus a shared expert: a small shape, and C5's
+    128 experts top-8 at 1024 tokens (hidden and FFN narrowed so the oracle is quick)."""
     R = _rules()
     r = rng(31)
-    tokens, hidden, experts, top, ffn = 384, 256, 16, 4, 128
     hb, h = bf16_bits_normal(r, (tokens, hidden))
     router_b, _ = bf16_bits_normal(r, (experts, hidden), 0.2)
     win_b, _ = bf16_bits_normal(r, (experts, 2 * ffn, hidden), 0.05)
