@@ -322,15 +322,27 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             float sv[4][4];
             float mx = -INFINITY;
             const int hi_off = (int)rpos[qt] - (int)kb, lo_off = (int)rfrom[qt] - (int)kb;
+            // One uniform branch a block: the masks only where a block meets a window's
+            // edge (a per-score short-circuit test compiled to a branch a score).
+            if (inside) {
 #pragma unroll
-            for (int kt = 0; kt < 4; kt++)
+                for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int k = kt * 16 + 4 * (int)grp + i;
-                    const bool ok = inside || (act[qt] && k <= hi_off && k >= lo_off);
-                    sv[kt][i] = ok ? s[kt][qt][i] * sl : -INFINITY;
-                    mx = fmaxf(mx, sv[kt][i]);
-                }
+                    for (int i = 0; i < 4; i++) {
+                        sv[kt][i] = s[kt][qt][i] * sl;
+                        mx = fmaxf(mx, sv[kt][i]);
+                    }
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int k = kt * 16 + 4 * (int)grp + i;
+                        const bool ok = act[qt] & (k <= hi_off) & (k >= lo_off);
+                        sv[kt][i] = ok ? s[kt][qt][i] * sl : -INFINITY;
+                        mx = fmaxf(mx, sv[kt][i]);
+                    }
+            }
             mx = rows4_max(mx);
             // The reference point m moves only when a score passes it by more than
             // kSlack (base 2): p = 2^(score - m) then stays below 2^kSlack, and most
