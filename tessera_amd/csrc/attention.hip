@@ -403,7 +403,7 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
     const uint32_t part = blockIdx.x, kvh = blockIdx.y, r = blockIdx.z, parts = gridDim.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
 
-    __shared__ __attribute__((aligned(16))) float sp[kLongWaves][G][16];
+    __shared__ __attribute__((aligned(16))) float sp[kLongWaves][G][32];  // p[head][key] of the current pair
     __shared__ float sm[kLongWaves][G], sl[kLongWaves][G];
     __shared__ __attribute__((aligned(16))) float so[kLongWaves][G][128];
     __shared__ uint32_t stab[kLongPages];
@@ -486,28 +486,37 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
 #pragma unroll
         for (int e = 0; e < 8; e++) o[h][e] = 0.0f;
 
-    // One 16-key block: scores on the matrix unit, online softmax, P*V on the VALU.
-    auto block = [&](uint32_t kb, const u32x4 (&kk)[4], const u32x4 (&vq)[4]) {
-        if (kb > pos || kb + 16 <= from) return;  // uniform across the wave
-        const uint32_t key = kb + col;
-        f32x4 sc = {0, 0, 0, 0};
+    // Two 16-key blocks (32 keys from kb): scores on the matrix unit, one online
+    // softmax update over both (one max and one sum reduction, one rescale of o),
+    // P*V on the VALU.
+    auto pair = [&](uint32_t kb, const LongBuf<G> &b) {
+        if (kb > pos || kb + 32 <= from) return;  // uniform across the wave
+        f32x4 sc[2];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            sc = mfma16(as_bf16x8(qh[j]), as_bf16x8(kk[j]), sc);
-            sc = mfma16(as_bf16x8(ql[j]), as_bf16x8(kk[j]), sc);
+        for (int t = 0; t < 2; t++) {
+            sc[t] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sc[t] = mfma16(as_bf16x8(qh[j]), as_bf16x8(b.kk[t][j]), sc[t]);
+                sc[t] = mfma16(as_bf16x8(ql[j]), as_bf16x8(b.kk[t][j]), sc[t]);
+            }
         }
-        const bool valid = key >= from && key <= pos;
+        const uint32_t key0 = kb + col, key1 = kb + 16 + col;
+        const bool valid0 = key0 >= from && key0 <= pos, valid1 = key1 >= from && key1 <= pos;
         float alpha[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float si = valid ? sc[i] * (p.scale * kLog2e) : -INFINITY;  // base 2
-            const float mn = fmaxf(m[i], row16_max(si));
-            alpha[i] = (mn == -INFINITY) ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
-            const float pi = (mn == -INFINITY || !valid) ? 0.0f : __builtin_amdgcn_exp2f(si - mn);
-            l[i] = l[i] * alpha[i] + row16_sum(pi);
+            const float s0 = valid0 ? sc[0][i] * (p.scale * kLog2e) : -INFINITY;  // base 2
+            const float s1 = valid1 ? sc[1][i] * (p.scale * kLog2e) : -INFINITY;
+            const float mn = fmaxf(m[i], row16_max(fmaxf(s0, s1)));
+            const bool none = mn == -INFINITY;
+            alpha[i] = none ? 1.0f : __builtin_amdgcn_exp2f(m[i] - mn);
+            const float p0 = (none || !valid0) ? 0.0f : __builtin_amdgcn_exp2f(s0 - mn);
+            const float p1 = (none || !valid1) ? 0.0f : __builtin_amdgcn_exp2f(s1 - mn);
+            l[i] = l[i] * alpha[i] + row16_sum(p0 + p1);
             m[i] = mn;
             const uint32_t h = 4 * grp + i;
-            if (h < G) sp[wave][h][col] = pi;
+            if (h < G) { sp[wave][h][col] = p0; sp[wave][h][16 + col] = p1; }
         }
         __builtin_amdgcn_wave_barrier();  // the wave reads back its own LDS writes
 #pragma unroll
@@ -517,21 +526,23 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
             for (int e = 0; e < 8; e++) o[h][e] *= a;
         }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t i = 4 * j + grp, kpos = kb + i;
-            const bool ok = kpos >= from && kpos <= pos;  // p is zero outside; keep v finite too
-            const u32x4 v = vq[j];
-            const uint32_t w4[4] = {ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int h = 0; h < G; h++) {
-                const float pk = sp[wave][h][i];
+            for (int j = 0; j < 4; j++) {
+                const uint32_t i = 4 * j + grp, kpos = kb + 16 * t + i;
+                const bool ok = kpos >= from && kpos <= pos;  // p is zero outside; keep v finite too
+                const u32x4 v = b.vq[t][j];
+                const uint32_t w4[4] = {ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u};
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    o[h][2 * e] += pk * lo_bf16(w4[e]);
-                    o[h][2 * e + 1] += pk * hi_bf16(w4[e]);
+                for (int h = 0; h < G; h++) {
+                    const float pk = sp[wave][h][16 * t + i];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        o[h][2 * e] += pk * lo_bf16(w4[e]);
+                        o[h][2 * e + 1] += pk * hi_bf16(w4[e]);
+                    }
                 }
             }
-        }
         __builtin_amdgcn_wave_barrier();
     };
 
@@ -543,15 +554,13 @@ __global__ __launch_bounds__(kLongWaves * 64) void attend_long_kernel(RowsParams
             load(kb0 + 32, buf[1].kk[0], buf[1].vq[0]);
             load(kb0 + 48, buf[1].kk[1], buf[1].vq[1]);
         }
-        block(kb0, buf[0].kk[0], buf[0].vq[0]);
-        block(kb0 + 16, buf[0].kk[1], buf[0].vq[1]);
+        pair(kb0, buf[0]);
         if (it + 1 >= iters) break;
         if (it + 2 < iters) {
             load(kb0 + 64, buf[0].kk[0], buf[0].vq[0]);
             load(kb0 + 80, buf[0].kk[1], buf[0].vq[1]);
         }
-        block(kb0 + 32, buf[1].kk[0], buf[1].vq[0]);
-        block(kb0 + 48, buf[1].kk[1], buf[1].vq[1]);
+        pair(kb0 + 32, buf[1]);
     }
 
     // Merge the waves of this group into its partial.
