@@ -97,6 +97,60 @@ TS_DEV u32x2 read_vt4(const char *a) {
     return __builtin_bit_cast(u32x2, v);
 }
 
+// Row groups this order-by-cost considers (beyond it: launch order).
+constexpr uint32_t kMaxOrder = 256;
+
+// The (row group << 16 | head group) of this block, widest key span first. Causal
+// prefill groups differ up to rows / 64 times in work and one 8-wave group fills a CU,
+// so launch order leaves a tail; every block ranks the row groups by the key blocks
+// they span (the positions come from L2) and takes, for its linear id L, the group of
+// rank L / gridDim.y and head group L % gridDim.y: the widest first, head groups
+// fastest (consecutive blocks go to different XCDs, each then keeps one head group's
+// keys in its L2). Ties keep row order. Every block computes the same ranking, so
+// the mapping is a permutation of the grid.
+TS_DEV uint32_t widest_first(const FlashParams &p, uint32_t lane, uint32_t wave, uint32_t waves) {
+    __shared__ uint32_t slo[kMaxOrder], shi[kMaxOrder], ssel;
+    const uint32_t ng = gridDim.x, nh = gridDim.y;
+    if (ng <= 1 || ng > kMaxOrder) return (blockIdx.x << 16) | blockIdx.y;
+    const uint32_t L = blockIdx.x + ng * blockIdx.y, target = L / nh;
+    for (uint32_t u = threadIdx.x; u < ng; u += 64 * waves) { slo[u] = 0xffffffffu; shi[u] = 0; }
+    if (threadIdx.x == 0) ssel = target;  // every rank is taken; set for form's sake
+    __syncthreads();
+    // One wave a 64-row half group at a time: the span [min from, max pos] of the
+    // group's rows (positions clamped to the bound; refused rows only widen it).
+    for (uint32_t half = wave; half < 2 * ng; half += waves) {
+        const uint32_t r = 64 * half + lane;
+        uint32_t hi = 0, lo = 0xffffffffu;
+        if (r < p.rows) {
+            hi = min(p.positions[r], p.max_position);
+            lo = hi > p.back ? hi - p.back : 0;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
+            lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
+        }
+        if (lane == 0 && lo <= hi) {
+            atomicMin(&slo[half >> 1], lo);
+            atomicMax(&shi[half >> 1], hi);
+        }
+    }
+    __syncthreads();
+    // Rank by the key blocks spanned (an upper bound for a group of several slots).
+    for (uint32_t g = threadIdx.x; g < ng; g += 64 * waves) {
+        auto cost = [&](uint32_t j) { return slo[j] <= shi[j] ? (shi[j] >> 6) - (slo[j] >> 6) + 1 : 0u; };
+        const uint32_t c = cost(g);
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ng; j++) {
+            const uint32_t cj = cost(j);
+            rank += (cj > c) | ((cj == c) & (j < g));
+        }
+        if (rank == target) ssel = g;
+    }
+    __syncthreads();
+    return (ssel << 16) | (L % nh);
+}
+
 // The transposed formulation: S^T = K Q^T and O^T = V^T P^T. With K as the A
 // operand (rows = keys) and Q^T as B (columns = queries), the S^T accumulator lane
 // (query col, group g) holds keys 4 g + i of each 16-key tile: after the softmax
@@ -118,9 +172,10 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), t = threadIdx.x;
     const uint32_t col = lane & 15, grp = lane >> 4;
-    const uint32_t G = p.heads / p.kv_heads, h = blockIdx.y * HG + (wave >> 2), kvh = h / G;
+    const uint32_t rg = widest_first(p, lane, wave, kWaves), hp = rg & 0xffffu;
+    const uint32_t G = p.heads / p.kv_heads, h = hp * HG + (wave >> 2), kvh = h / G;
     const uint32_t qw = wave & 3;  // the wave's 16 kQT rows within the group's kRows
-    const uint32_t r0 = blockIdx.x * kRows;
+    const uint32_t r0 = (rg >> 16) * kRows;
     constexpr uint32_t kNoPass = 0xffffffffu;
 
     // Passes: one per distinct slot among the group's rows, numbered in order of first
