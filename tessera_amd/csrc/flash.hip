@@ -244,6 +244,13 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     __syncthreads();
     const uint32_t npass = snpass;
 
+    // The scale's sign goes into q (exact: a sign flip of every bf16 / f32 value), so
+    // the scores are scaled by sl >= 0 and a maximum of raw scores is one of scaled
+    // ones. A zero scale becomes 2^-100 (every p equal to 1 within f32 rounding for
+    // any finite score below 2^75), so masked -inf scores stay -inf.
+    const uint32_t qsign = p.scale < 0.0f ? 0x80008000u : 0u;
+    const float sl = p.scale == 0.0f ? 0x1p-100f : fabsf(p.scale) * 1.4426950408889634f;  // to base 2
+
     // This wave's queries: r0 + 16 kQT wave + 16 qt + col. The q operand
     // (B, columns = queries), loaded once: lane group g holds d 32 g + 8 j .. + 8 for
     // d-step j; bf16 q as is, f32 q as two exact bf16 parts.
@@ -261,7 +268,8 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             const uint16_t *qr = (const uint16_t *)p.q + ((size_t)(rlive[qt] ? r : 0) * p.heads + h) * 128 + 32 * grp;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                qh[qt][j] = rlive[qt] ? *(const u32x4 *)(qr + 8 * j) : u32x4{0, 0, 0, 0};
+                const u32x4 w = rlive[qt] ? *(const u32x4 *)(qr + 8 * j) : u32x4{0, 0, 0, 0};
+                qh[qt][j] = u32x4{w.x ^ qsign, w.y ^ qsign, w.z ^ qsign, w.w ^ qsign};
                 ql[qt][j] = u32x4{0, 0, 0, 0};
             }
         } else {
@@ -272,6 +280,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     float a = rlive[qt] ? qr[8 * j + 2 * e] : 0.0f, b = rlive[qt] ? qr[8 * j + 2 * e + 1] : 0.0f;
+                    if (qsign) { a = -a; b = -b; }
                     float ha = bf16_round(a), hb = bf16_round(b);
                     hh[e] = pack_bf16x2(ha, hb);
                     ll[e] = pack_bf16x2(a - ha, b - hb);
@@ -290,7 +299,6 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     for (int j = 0; j < 4; j++) koff[j] = col * 256 + (((4 * grp + j) ^ col) << 4);
     const uint32_t vk = 4 * grp + (col >> 2), vbase = vk * 256 + 8 * (col & 1), vc = (col & 3) >> 1;
 
-    const float sl = p.scale * 1.4426950408889634f;  // scores to base 2
     float m[kQT], l[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) { m[qt] = -INFINITY; l[qt] = 0.0f; }
@@ -374,31 +382,30 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         bf16x8 ph[2][kQT], pl[2][kQT];
 #pragma unroll
         for (int qt = 0; qt < kQT; qt++) {
-            float sv[4][4];
-            float mx = -INFINITY;
             const int hi_off = (int)rpos[qt] - (int)kb, lo_off = (int)rfrom[qt] - (int)kb;
             // One uniform branch a block: the masks only where a block meets a window's
-            // edge (a per-score short-circuit test compiled to a branch a score).
-            if (inside) {
-#pragma unroll
-                for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        sv[kt][i] = s[kt][qt][i] * sl;
-                        mx = fmaxf(mx, sv[kt][i]);
-                    }
-            } else {
+            // edge (a per-score short-circuit test compiled to a branch a score). The
+            // scores stay raw (sl >= 0: the sign of the scale is in q), masked ones -inf
+            // in place.
+            if (!inside) {
 #pragma unroll
                 for (int kt = 0; kt < 4; kt++)
 #pragma unroll
                     for (int i = 0; i < 4; i++) {
                         const int k = kt * 16 + 4 * (int)grp + i;
                         const bool ok = act[qt] & (k <= hi_off) & (k >= lo_off);
-                        sv[kt][i] = ok ? s[kt][qt][i] * sl : -INFINITY;
-                        mx = fmaxf(mx, sv[kt][i]);
+                        s[kt][qt][i] = ok ? s[kt][qt][i] : -INFINITY;
                     }
             }
-            mx = rows4_max(mx);
+            float mx;
+            {
+                float t[4];
+#pragma unroll
+                for (int kt = 0; kt < 4; kt++)
+                    t[kt] = fmaxf(fmaxf(s[kt][qt][0], s[kt][qt][1]), fmaxf(s[kt][qt][2], s[kt][qt][3]));
+                mx = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
+            }
+            mx = rows4_max(mx) * sl;  // -inf stays -inf (sl > 0)
             // The reference point m moves only when a score passes it by more than
             // kSlack (base 2): p = 2^(score - m) then stays below 2^kSlack, and most
             // blocks leave l and O unscaled (O / l does not depend on the choice of m).
@@ -406,7 +413,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             const float mn = raise ? mx : m[qt];
             const float alpha = raise ? __builtin_amdgcn_exp2f(m[qt] - mn) : 1.0f;  // 0 from m = -inf
             const float mo = mn == -INFINITY ? 0.0f : mn;  // exp2(-inf - 0) = 0 for masked keys
-            float sum = 0.0f;
+            float part[4];  // sums of p by 16-key tile, then as a tree
 #pragma unroll
             for (int st = 0; st < 2; st++) {
                 uint32_t hw[4], lw[4];
@@ -415,10 +422,10 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
 #pragma unroll
                     for (int i = 0; i < 4; i += 2) {
                         const int kt = 2 * st + tt;
-                        const float pa = __builtin_amdgcn_exp2f(sv[kt][i] - mo);
-                        const float pb = __builtin_amdgcn_exp2f(sv[kt][i + 1] - mo);
-                        sum += pa;
-                        sum += pb;
+                        // 2^(score - m) = 2^(s sl - mo): one fma; a masked -inf gives 0.
+                        const float pa = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i], sl, -mo));
+                        const float pb = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][i + 1], sl, -mo));
+                        part[kt] = i == 0 ? pa + pb : part[kt] + (pa + pb);
                         // p in [0, 2^kSlack] (never NaN for finite scores): the
                         // plain round-to-nearest-even conversion, no NaN fix-up.
                         hw[2 * tt + i / 2] = __builtin_bit_cast(
@@ -434,7 +441,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
                 ph[st][qt] = as_bf16x8(u32x4{hw[0], hw[1], hw[2], hw[3]});
                 pl[st][qt] = as_bf16x8(u32x4{lw[0], lw[1], lw[2], lw[3]});
             }
-            sum = rows4_sum(sum);
+            const float sum = rows4_sum((part[0] + part[1]) + (part[2] + part[3]));
             l[qt] = l[qt] * alpha + sum;
             m[qt] = mn;
             // Rescale O only when some query of the wave moved its reference point.
