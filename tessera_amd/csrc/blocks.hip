@@ -167,6 +167,118 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
     else ((float *)p.out)[at] = v;
 }
 
+typedef __attribute__((address_space(3))) void block_lds_void;
+
+constexpr uint32_t kShortBytes = 9216;  // LDS bytes of one wave's rows (short form)
+
+// Rows a pass and passes a wave of the short form with L lanes a row: 16 rows a wave
+// (8 at L = 32, so the rows' bytes fit kShortBytes).
+constexpr int short_np(int L) { return L == 32 ? 4 : L == 16 ? 4 : 2; }
+
+// Short rows (at most 32 blocks, e.g. 1024 codes of 32-code blocks, or of 128-code
+// ones): L lanes a row (nb <= L), 64 / L rows a pass, so every lane decodes a block
+// where the form above would leave 64 - nb lanes idle. A wave's NP passes (RT rows)
+// are contiguous bytes: they go straight to LDS (4-byte global_load_lds, lane i of an
+// instruction at 4 i: no staging registers); a lane then runs its NP blocks (same
+// block index, NP rows) as NP interleaved chains over one load of x. The arithmetic
+// per block and the block-order sum of each output are those of block_gemv_kernel,
+// so both give the same bits.
+template <int F, int M, bool XF32, int L>
+__global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockParams p) {
+#pragma clang fp contract(off)
+    using BF = BlockForm<F>;
+    constexpr int B = BF::B, BB = BF::BB, SB = BF::SB;
+    constexpr int P = B < 32 ? B : 32;
+    constexpr int G = 64 / L, NP = short_np(L), RT = G * NP;
+    static_assert(RT * M <= 64, "one lane an output");
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kShortBytes / 4];
+    __shared__ __attribute__((aligned(16))) float contrib[kWaves][RT * M][L];
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t r0 = (blockIdx.x * kWaves + wave) * RT;  // this wave's RT rows
+    if (r0 >= p.n) return;  // waves are independent: no group barrier below
+    const uint32_t K = p.k, N = p.n, Mr = p.m, nb = K / B;
+    const uint32_t nrows = min((uint32_t)RT, N - r0);
+    const uint32_t words = nrows * (nb * BB / 4);
+    const uint32_t *src = (const uint32_t *)(p.w + BF::HEAD + (size_t)r0 * nb * BB);
+    char *base = (char *)stage[wave];
+    for (uint32_t w0 = 0; w0 < words; w0 += 64) {
+        const uint32_t i = min(w0 + lane, words - 1);  // past the end: a repeat, unused
+        __builtin_amdgcn_global_load_lds((const void *)(src + i), (block_lds_void *)(base + 4 * w0), 4, 0, 0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+
+    const uint32_t b = lane % L, g = lane / L;
+    if (b < nb) {
+        const uint32_t k0 = b * B;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if ((uint32_t)m >= Mr) break;
+            float part[NP];
+#pragma unroll
+            for (int i = 0; i < NP; i++) part[i] = 0.0f;
+            // Block::dot's part: x_j times code j, summed from 0.0 in j order.
+#pragma unroll
+            for (int q = 0; q < B / P; q++) {
+                float xv[P];
+                load_x<P, XF32>(p.x, (size_t)m * K + k0 + q * P, xv);
+#pragma unroll
+                for (int i = 0; i < NP; i++) {
+                    const uint32_t rr = min(i * G + g, nrows - 1);  // rows past the end: unused
+                    float wv[P];
+                    block_codes<F, P>((const uint8_t *)stage[wave] + (size_t)(rr * nb + b) * BB + SB, q, wv);
+#pragma unroll
+                    for (int j = 0; j < P; j++) part[i] = part[i] + xv[j] * wv[j];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                const uint32_t rr = i * G + g;
+                const uint8_t *blk = (const uint8_t *)stage[wave] + (size_t)(min(rr, nrows - 1) * nb + b) * BB;
+                contrib[wave][rr * M + m][b] = block_scale<F>(blk) * part[i];
+            }
+        }
+    }
+    wave_lds_sync();
+    // Lane rr * M + m: output (m, r0 + rr), its blocks' contributions in block order.
+    const uint32_t rr = lane / M, m = lane % M;
+    if (lane >= RT * M || rr >= nrows || m >= Mr) return;
+    const float *cv = contrib[wave][lane];
+    float run = 0.0f;
+    for (uint32_t j = 0; j < nb; j++) run = run + cv[j];
+    const float head = BF::HEAD ? *(const float *)p.w : 1.0f;  // Block::dot: head * sum
+    float v = head * run;
+    const size_t at = (size_t)m * N + r0 + rr;
+    if (p.stages & TS_AFTER_ADD) v += p.a0[at];
+    if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
+    else ((float *)p.out)[at] = v;
+}
+
+using ShortKern = void (*)(BlockParams);
+
+template <int F, bool XF32, int L>
+ShortKern short_m(uint32_t m) {
+    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, L>
+         : m == 2 ? block_gemv_short_kernel<F, 2, XF32, L> : block_gemv_short_kernel<F, 4, XF32, L>;
+}
+
+// The short form for nb <= 32 blocks a row whose wave rows fit kShortBytes, or NULL.
+template <int F>
+ShortKern short_pick(uint32_t m, bool xf, uint32_t nb) {
+    const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
+    if (nb > 32 || (uint64_t)(64 / L) * short_np(L) * nb * BlockForm<F>::BB > kShortBytes) return nullptr;
+    if (L == 8) return xf ? short_m<F, true, 8>(m) : short_m<F, false, 8>(m);
+    if (L == 16) return xf ? short_m<F, true, 16>(m) : short_m<F, false, 16>(m);
+    return xf ? short_m<F, true, 32>(m) : short_m<F, false, 32>(m);
+}
+
+// Rows a wave of the short form for nb blocks a row.
+inline uint32_t short_rows(uint32_t nb) {
+    const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
+    return (64 / L) * short_np(L);
+}
+
 using Kern = void (*)(BlockParams);
 
 template <int F, bool XF32>
@@ -218,6 +330,23 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     const bool xf = a->x_dtype == TS_F32;
+    const uint32_t nb = a->k / block_shape(a->w_dtype).block;
+    ShortKern sk = nullptr;
+    switch (a->w_dtype) {
+    case TS_Q8_0: sk = short_pick<0>(a->m, xf, nb); break;
+    case TS_MXFP8: sk = short_pick<1>(a->m, xf, nb); break;
+    case TS_INT4_G32: sk = short_pick<2>(a->m, xf, nb); break;
+    case TS_Q4_0: sk = short_pick<3>(a->m, xf, nb); break;
+    case TS_NVFP4: sk = short_pick<4>(a->m, xf, nb); break;
+    case TS_MXFP4: sk = short_pick<5>(a->m, xf, nb); break;
+    default: sk = short_pick<6>(a->m, xf, nb); break;
+    }
+    if (sk) {
+        const uint32_t waves = (a->n + short_rows(nb) - 1) / short_rows(nb);
+        hipLaunchKernelGGL(sk, dim3((waves + kWaves - 1) / kWaves), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
+        TS_CHECK_LAUNCH("lanes (block form, short rows) launch");
+        return TS_OK;
+    }
     Kern k;
     switch (a->w_dtype) {
     case TS_Q8_0: k = pick_x<0>(a->m, xf); break;
