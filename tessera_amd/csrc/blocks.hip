@@ -169,7 +169,7 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
 
 typedef __attribute__((address_space(3))) void block_lds_void;
 
-constexpr uint32_t kShortBytes = 9216;  // LDS bytes of one wave's rows (short form)
+constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; + 16 of pad: 9 KiB)
 
 // Rows a pass and passes a wave of the short form with L lanes a row: 16 rows a wave
 // (8 at L = 32, so the rows' bytes fit kShortBytes).
@@ -191,7 +191,8 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     constexpr int P = B < 32 ? B : 32;
     constexpr int G = 64 / L, NP = short_np(L), RT = G * NP;
     static_assert(RT * M <= 64, "one lane an output");
-    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kShortBytes / 4];
+    // One word past the rows: the aligned word reads of the last block's codes.
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kShortBytes / 4 + 4];
     __shared__ __attribute__((aligned(16))) float contrib[kWaves][RT * M][L];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -227,7 +228,26 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
                 for (int i = 0; i < NP; i++) {
                     const uint32_t rr = min(i * G + g, nrows - 1);  // rows past the end: unused
                     float wv[P];
-                    block_codes<F, P>((const uint8_t *)stage[wave] + (size_t)(rr * nb + b) * BB + SB, q, wv);
+                    if (BF::BITS == 8) {
+                        // Byte codes from aligned LDS words: words d[0..P/4] around them,
+                        // each 4 codes one alignbyte, then 4 converts (no byte reads).
+                        const uint32_t off = (rr * nb + b) * BB + SB + q * P, w0 = off >> 2, sh = off & 3u;
+                        uint32_t d[P / 4 + 1];
+#pragma unroll
+                        for (int e = 0; e <= P / 4; e++) d[e] = stage[wave][w0 + e];
+#pragma unroll
+                        for (int e = 0; e < P / 4; e++) {
+                            const uint32_t w = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
+                            if (BF::CODE == kCodeI8) {
+#pragma unroll
+                                for (int t = 0; t < 4; t++) wv[4 * e + t] = (float)((int32_t)(w << (24 - 8 * t)) >> 24);
+                            } else {
+                                e4m3x4_float(w, wv + 4 * e);
+                            }
+                        }
+                    } else {
+                        block_codes<F, P>((const uint8_t *)stage[wave] + (size_t)(rr * nb + b) * BB + SB, q, wv);
+                    }
 #pragma unroll
                     for (int j = 0; j < P; j++) part[i] = part[i] + xv[j] * wv[j];
                 }

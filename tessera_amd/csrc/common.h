@@ -95,13 +95,18 @@ TS_DEV float bf16_round(float x) { return bf16_float(bf16_bits(x)); }
 TS_DEV float lo_bf16(uint32_t v) { return __uint_as_float(v << 16); }
 TS_DEV float hi_bf16(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
-// OCP e4m3 code -> f32. Placing the 7 magnitude bits at f32 bits 20..26 gives
-// 2^(e-127)(1+m/8) for e>0 and the f32 subnormal m/8*2^-126 for e=0; one
-// multiply by 2^120 rebiases both cases exactly. Code 0x7F (NaN) is never
-// produced by the saturating quantizer and is not special-cased here.
-TS_DEV float e4m3_float(uint32_t c) {
-    float mag = __uint_as_float((c & 0x7fu) << 20) * 0x1p120f;
-    return (c & 0x80u) ? -mag : mag;
+typedef float ts_f32x2_t __attribute__((ext_vector_type(2)));
+
+// OCP e4m3 (e4m3fn) code -> f32 on gfx950's conversion (scale 1.0: exact, subnormals
+// included); codes 0x7F / 0xFF give NaN, as the format defines (and the interpreter's
+// widening does).
+TS_DEV float e4m3_float(uint32_t c) { return __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(c, 1.0f, false)[0]; }
+
+// Four e4m3 codes (byte order) -> four f32, the same conversion two at a time.
+TS_DEV void e4m3x4_float(uint32_t w, float *f) {
+    const ts_f32x2_t lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
+    const ts_f32x2_t hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, true);
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
 }
 
 // Four e4m3 codes (one u32) -> two packed bf16 pairs (exact: 3 mantissa bits).
@@ -118,7 +123,7 @@ TS_DEV u32x2 e4m3x4_to_bf16x4(uint32_t w) {
 TS_DEV void e4m3x4_to_f32(uint32_t w, float *f) {
     typedef float f32x2_t __attribute__((ext_vector_type(2)));
     const f32x2_t lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false), hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-    f[0] = lo.x; f[1] = lo.y; f[2] = hi.x; f[3] = hi.y;
+    f[0] = lo[0]; f[1] = lo[1]; f[2] = hi[0]; f[3] = hi[1];
 }
 
 // The argmax key of entry n with value v, ordered as the pick (argmax_spans):

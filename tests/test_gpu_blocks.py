@@ -61,6 +61,25 @@ def test_block_product_bf16_rows_add_and_bf16_out(form):
     assert np.array_equal(got16, O.bf16_widen(O.bf16_narrow(want)))
 
 
+@pytest.mark.parametrize("k", [1024, 8192])
+def test_block_product_e4m3_nan_codes(k):
+    """e4m3 0x7F / 0xFF are NaN (e4m3fn; the interpreter's widening): a hand-placed
+    NaN code (mxfp8) or block scale (nvfp4) makes exactly its row NaN, as in the
+    oracle, on the short-row (k 1024) and the long-row (k 8192) forms."""
+    from tessera_amd import rules as R
+    n, m = 40, 2
+    for form, bb, head, at in (("mxfp8", 33, 0, 1 + 5), ("nvfp4", 9, 4, 0)):
+        xf, xd, wb = _case(form, m, n, k, 11)
+        wb = wb.copy()
+        nb = k // O.block_size(form)
+        for row, blk, code in ((3, 2, 0x7F), (17, nb - 1, 0xFF)):
+            wb[head + (row * nb + blk) * bb + at] = code
+        want = O.block_product(form, xf, wb, n)
+        assert np.isnan(want[:, 3]).all() and np.isnan(want[:, 17]).all()
+        got = from_dev(R.lanes(to_dev(xd, torch), _dev(wb), w_form=form, rows=n))
+        np.testing.assert_array_equal(got, want)
+
+
 def _lane(form, k):
     return 2 * k / O.block_size(form) + 8
 
