@@ -169,6 +169,10 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
 
 typedef __attribute__((address_space(3))) void block_lds_void;
 
+// e2m1 codes of byte T of w (low nibble first) as f32 (scale 1: exact).
+template <int T>
+TS_DEV ts_f32x2_t fp4_pair(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, T); }
+
 constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; + 16 of pad: 9 KiB)
 
 // Rows a pass and passes a wave of the short form with L lanes a row: 16 rows a wave
@@ -246,7 +250,37 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
                             }
                         }
                     } else {
-                        block_codes<F, P>((const uint8_t *)stage[wave] + (size_t)(rr * nb + b) * BB + SB, q, wv);
+                        // Nibble codes the same way: P / 2 bytes in aligned words, byte i
+                        // holding codes 2 i, 2 i + 1 (low nibble first), or i and i + B / 2
+                        // (q4_0's halves).
+                        const uint32_t off = (rr * nb + b) * BB + SB + q * (P / 2), w0 = off >> 2, sh = off & 3u;
+                        uint32_t d[P / 8 + 1];
+#pragma unroll
+                        for (int e = 0; e <= P / 8; e++) d[e] = stage[wave][w0 + e];
+#pragma unroll
+                        for (int e = 0; e < P / 8; e++) {
+                            const uint32_t w = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
+#pragma unroll
+                            for (int t = 0; t < 4; t++) {
+                                const int i = 4 * e + t;  // byte of the piece
+                                if (BF::CODE == kCodeE2M1) {
+                                    const ts_f32x2_t v = t == 0 ? fp4_pair<0>(w) : t == 1 ? fp4_pair<1>(w)
+                                                       : t == 2 ? fp4_pair<2>(w) : fp4_pair<3>(w);
+                                    wv[2 * i] = v[0];
+                                    wv[2 * i + 1] = v[1];
+                                } else {
+                                    const float lo = (float)((w >> (8 * t)) & 15u) - 8.0f;
+                                    const float hi = (float)((w >> (8 * t + 4)) & 15u) - 8.0f;
+                                    if (BF::HALVES) {
+                                        wv[i] = lo;
+                                        wv[i + P / 2] = hi;
+                                    } else {
+                                        wv[2 * i] = lo;
+                                        wv[2 * i + 1] = hi;
+                                    }
+                                }
+                            }
+                        }
                     }
 #pragma unroll
                     for (int j = 0; j < P; j++) part[i] = part[i] + xv[j] * wv[j];
