@@ -231,6 +231,19 @@ def test_prefill_flash_rows_packed(lens):
     np.testing.assert_allclose(run("flash", c, s), want(c, s), atol=ATOL, rtol=0)
 
 
+@pytest.mark.parametrize("prompts", [200, 262])
+def test_prefill_flash_rows_many_groups(prompts):
+    """Hundreds of ragged prompts packed back to back (lengths 100..156): 200 prompts
+    give ~200 128-row groups that the kernel ranks by their key spans and runs widest
+    first; 262 give more groups than it ranks (256), which run in launch order. Every
+    row is checked against the oracle (2 q heads over 1 kv head keep it small)."""
+    lens = [100 + (i * 37) % 57 for i in range(prompts)]
+    assert (sum(lens) + 127) // 128 > 256 if prompts == 262 else (sum(lens) + 127) // 128 <= 256
+    c = paged_case(prompts, lens, heads=2, kv_heads=1, pos=_packed(lens))
+    s = 1 / math.sqrt(128)
+    np.testing.assert_allclose(run("flash", c, s), want(c, s), atol=ATOL, rtol=0)
+
+
 def test_prefill_flash_rows_interleaved_slots():
     """Rows of two slots interleaved row by row (slots not in runs), a window of 50."""
     n = 150
