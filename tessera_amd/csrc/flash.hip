@@ -109,40 +109,53 @@ constexpr uint32_t kMaxOrder = 256;
 // keys in its L2). Ties keep row order. Every block computes the same ranking, so
 // the mapping is a permutation of the grid.
 TS_DEV uint32_t widest_first(const FlashParams &p, uint32_t lane, uint32_t wave, uint32_t waves) {
-    __shared__ uint32_t slo[kMaxOrder], shi[kMaxOrder], ssel;
+    __shared__ uint32_t slo[kMaxOrder], shi[kMaxOrder], scost[kMaxOrder], ssel;
     const uint32_t ng = gridDim.x, nh = gridDim.y;
     if (ng <= 1 || ng > kMaxOrder) return (blockIdx.x << 16) | blockIdx.y;
     const uint32_t L = blockIdx.x + ng * blockIdx.y, target = L / nh;
     for (uint32_t u = threadIdx.x; u < ng; u += 64 * waves) { slo[u] = 0xffffffffu; shi[u] = 0; }
     if (threadIdx.x == 0) ssel = target;  // every rank is taken; set for form's sake
     __syncthreads();
-    // One wave a 64-row half group at a time: the span [min from, max pos] of the
-    // group's rows (positions clamped to the bound; refused rows only widen it).
-    for (uint32_t half = wave; half < 2 * ng; half += waves) {
-        const uint32_t r = 64 * half + lane;
-        uint32_t hi = 0, lo = 0xffffffffu;
-        if (r < p.rows) {
-            hi = min(p.positions[r], p.max_position);
-            lo = hi > p.back ? hi - p.back : 0;
+    // One wave a 64-row half group at a time, eight halves' positions loaded before
+    // any is reduced: the span [min from, max pos] of the group's rows (positions
+    // clamped to the bound; refused rows only widen it).
+    for (uint32_t h0 = wave; h0 < 2 * ng; h0 += 8 * waves) {
+        uint32_t his[8], los[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const uint32_t half = h0 + u * waves, r = 64 * half + lane;
+            his[u] = 0;
+            los[u] = 0xffffffffu;
+            if (half < 2 * ng && r < p.rows) {
+                his[u] = min(p.positions[r], p.max_position);
+                los[u] = his[u] > p.back ? his[u] - p.back : 0;
+            }
         }
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
-            lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
-        }
-        if (lane == 0 && lo <= hi) {
-            atomicMin(&slo[half >> 1], lo);
-            atomicMax(&shi[half >> 1], hi);
+        for (int u = 0; u < 8; u++) {
+            uint32_t hi = his[u], lo = los[u];
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                hi = max(hi, (uint32_t)__shfl_xor((int)hi, o, 64));
+                lo = min(lo, (uint32_t)__shfl_xor((int)lo, o, 64));
+            }
+            const uint32_t half = h0 + u * waves;
+            if (lane == 0 && half < 2 * ng && lo <= hi) {
+                atomicMin(&slo[half >> 1], lo);
+                atomicMax(&shi[half >> 1], hi);
+            }
         }
     }
     __syncthreads();
     // Rank by the key blocks spanned (an upper bound for a group of several slots).
+    for (uint32_t g = threadIdx.x; g < ng; g += 64 * waves)
+        scost[g] = slo[g] <= shi[g] ? (shi[g] >> 6) - (slo[g] >> 6) + 1 : 0u;
+    __syncthreads();
     for (uint32_t g = threadIdx.x; g < ng; g += 64 * waves) {
-        auto cost = [&](uint32_t j) { return slo[j] <= shi[j] ? (shi[j] >> 6) - (slo[j] >> 6) + 1 : 0u; };
-        const uint32_t c = cost(g);
+        const uint32_t c = scost[g];
         uint32_t rank = 0;
         for (uint32_t j = 0; j < ng; j++) {
-            const uint32_t cj = cost(j);
+            const uint32_t cj = scost[j];
             rank += (cj > c) | ((cj == c) & (j < g));
         }
         if (rank == target) ssel = g;
