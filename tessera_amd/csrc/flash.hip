@@ -513,6 +513,8 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
     TS_REQUIRE(ts::aligned(a->k, 16) && ts::aligned(a->v, 16) && ts::aligned(a->q, 16),
                "flash_rows: q, k, v must be 16-byte aligned");
     TS_REQUIRE(a->heads <= 65535, "flash_rows: grid limits");
+    // The block order packs a row group in 16 bits (65535 groups of 128 rows).
+    TS_REQUIRE(a->rows <= 65535u * 128u, "flash_rows: %u rows in one launch (at most %u)", a->rows, 65535u * 128u);
     if (a->rows == 0) return TS_OK;
     FlashParams p;
     p.q = a->q; p.k = (const uint16_t *)a->k; p.v = (const uint16_t *)a->v;

@@ -150,3 +150,23 @@ def test_dtype_enum_matches_header():
                      "TS_Q8_0": abi.TS_Q8_0, "TS_MXFP8": abi.TS_MXFP8, "TS_INT4_G32": abi.TS_INT4_G32,
                      "TS_Q4_0": abi.TS_Q4_0, "TS_NVFP4": abi.TS_NVFP4, "TS_MXFP4": abi.TS_MXFP4,
                      "TS_INT4_G128": abi.TS_INT4_G128}
+
+
+def test_flash_rows_refuses_more_row_groups_than_its_order_packs():
+    """flash_rows orders its blocks by a 16-bit row-group index: more than 65535 groups
+    of 128 rows are refused with TS_ERR_ARG before anything launches (fake device
+    addresses suffice). Skipped where a GPU is visible, as for the test above."""
+    import pytest
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("fake device addresses are only passed where no GPU could run them")
+    lib = abi.load()
+    r = abi.RowsArgs()
+    fake = 1 << 20
+    r.q = r.k = r.v = r.out = r.slots = r.positions = fake
+    r.heads, r.kv_heads, r.width, r.keys = 16, 8, 128, 1 << 20
+    r.scale, r.q_dtype, r.kv_dtype, r.out_dtype = 0.088, abi.TS_BF16, abi.TS_BF16, abi.TS_F32
+    r.max_position = (1 << 20) - 1
+    r.rows = 65535 * 128 + 1
+    assert lib.tessera_hip_flash_rows(C.byref(r), None) == abi.TS_ERR_ARG
+    assert b"rows in one launch" in lib.tessera_hip_last_error()
