@@ -187,13 +187,13 @@ constexpr int short_np(int L) { return L == 32 ? 4 : L == 16 ? 4 : 2; }
 // block index, NP rows) as NP interleaved chains over one load of x. The arithmetic
 // per block and the block-order sum of each output are those of block_gemv_kernel,
 // so both give the same bits.
-template <int F, int M, bool XF32, int L>
+template <int F, int M, bool XF32, int L, int NP>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockParams p) {
 #pragma clang fp contract(off)
     using BF = BlockForm<F>;
     constexpr int B = BF::B, BB = BF::BB, SB = BF::SB;
     constexpr int P = B < 32 ? B : 32;
-    constexpr int G = 64 / L, NP = short_np(L), RT = G * NP;
+    constexpr int G = 64 / L, RT = G * NP;
     static_assert(RT * M <= 64, "one lane an output");
     // One word past the rows: the aligned word reads of the last block's codes.
     __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kShortBytes / 4 + 4];
@@ -311,26 +311,33 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
 
 using ShortKern = void (*)(BlockParams);
 
-template <int F, bool XF32, int L>
+template <int F, bool XF32, int L, int NP = short_np(L)>
 ShortKern short_m(uint32_t m) {
-    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, L>
-         : m == 2 ? block_gemv_short_kernel<F, 2, XF32, L> : block_gemv_short_kernel<F, 4, XF32, L>;
+    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, L, NP>
+         : m == 2 ? block_gemv_short_kernel<F, 2, XF32, L, NP> : block_gemv_short_kernel<F, 4, XF32, L, NP>;
 }
 
 // The short form for nb <= 32 blocks a row whose wave rows fit kShortBytes, or NULL.
 template <int F>
 ShortKern short_pick(uint32_t m, bool xf, uint32_t nb) {
     const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
-    if (nb > 32 || (uint64_t)(64 / L) * short_np(L) * nb * BlockForm<F>::BB > kShortBytes) return nullptr;
+    if (nb > 32) return nullptr;
+    if ((uint64_t)(64 / L) * short_np(L) * nb * BlockForm<F>::BB > kShortBytes) {
+        // Wide blocks (128 codes): 2 passes of 2 rows at L = 32 (4 rows a wave).
+        if (L == 32 && (uint64_t)2 * 2 * nb * BlockForm<F>::BB <= kShortBytes)
+            return xf ? short_m<F, true, 32, 2>(m) : short_m<F, false, 32, 2>(m);
+        return nullptr;
+    }
     if (L == 8) return xf ? short_m<F, true, 8>(m) : short_m<F, false, 8>(m);
     if (L == 16) return xf ? short_m<F, true, 16>(m) : short_m<F, false, 16>(m);
     return xf ? short_m<F, true, 32>(m) : short_m<F, false, 32>(m);
 }
 
 // Rows a wave of the short form for nb blocks a row.
-inline uint32_t short_rows(uint32_t nb) {
+inline uint32_t short_rows(uint32_t nb, uint32_t bb) {
     const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
-    return (64 / L) * short_np(L);
+    const uint32_t rows = (64 / L) * short_np(L);
+    return rows * nb * bb > kShortBytes ? 4u : rows;  // the 2-pass form of short_pick
 }
 
 using Kern = void (*)(BlockParams);
@@ -396,7 +403,8 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     default: sk = short_pick<6>(a->m, xf, nb); break;
     }
     if (sk) {
-        const uint32_t waves = (a->n + short_rows(nb) - 1) / short_rows(nb);
+        const uint32_t rows = short_rows(nb, block_shape(a->w_dtype).bytes);
+        const uint32_t waves = (a->n + rows - 1) / rows;
         hipLaunchKernelGGL(sk, dim3((waves + kWaves - 1) / kWaves), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
         TS_CHECK_LAUNCH("lanes (block form, short rows) launch");
         return TS_OK;
