@@ -187,7 +187,7 @@ constexpr int short_np(int L) { return L == 32 ? 4 : L == 16 ? 4 : 2; }
 // block index, NP rows) as NP interleaved chains over one load of x. The arithmetic
 // per block and the block-order sum of each output are those of block_gemv_kernel,
 // so both give the same bits.
-template <int F, int M, bool XF32, int L, int NP>
+template <int F, int M, bool XF32, int L, int NP, uint32_t SBYTES = kShortBytes>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockParams p) {
 #pragma clang fp contract(off)
     using BF = BlockForm<F>;
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     constexpr int G = 64 / L, RT = G * NP;
     static_assert(RT * M <= 64, "one lane an output");
     // One word past the rows: the aligned word reads of the last block's codes.
-    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kShortBytes / 4 + 4];
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][SBYTES / 4 + 4];
     __shared__ __attribute__((aligned(16))) float contrib[kWaves][RT * M][L];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -311,10 +311,18 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
 
 using ShortKern = void (*)(BlockParams);
 
-template <int F, bool XF32, int L, int NP = short_np(L)>
+template <int F, bool XF32, int L, int NP = short_np(L), uint32_t SBYTES = kShortBytes>
 ShortKern short_m(uint32_t m) {
-    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, L, NP>
-         : m == 2 ? block_gemv_short_kernel<F, 2, XF32, L, NP> : block_gemv_short_kernel<F, 4, XF32, L, NP>;
+    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, L, NP, SBYTES>
+         : m == 2 ? block_gemv_short_kernel<F, 2, XF32, L, NP, SBYTES>
+                  : block_gemv_short_kernel<F, 4, XF32, L, NP, SBYTES>;
+}
+
+// L = 8 with 4 passes of 8 rows (32 rows a wave, 32 m outputs at most: m <= 2).
+template <int F, bool XF32>
+ShortKern short_l8_wide(uint32_t m) {
+    return m == 1 ? block_gemv_short_kernel<F, 1, XF32, 8, 4, 2 * kShortBytes>
+                  : block_gemv_short_kernel<F, 2, XF32, 8, 4, 2 * kShortBytes>;
 }
 
 // The short form for nb <= 32 blocks a row whose wave rows fit kShortBytes, or NULL.
@@ -328,15 +336,22 @@ ShortKern short_pick(uint32_t m, bool xf, uint32_t nb) {
             return xf ? short_m<F, true, 32, 2>(m) : short_m<F, false, 32, 2>(m);
         return nullptr;
     }
-    if (L == 8) return xf ? short_m<F, true, 8>(m) : short_m<F, false, 8>(m);
+    if (L == 8) {
+        // 128-code blocks: 4 passes of 8 rows (a wave's 32 rows in 17 KiB, two groups a
+        // CU) instead of 2.
+        if (BlockForm<F>::B == 128 && m <= 2 && (uint64_t)32 * nb * BlockForm<F>::BB <= 2 * kShortBytes)
+            return xf ? short_l8_wide<F, true>(m) : short_l8_wide<F, false>(m);
+        return xf ? short_m<F, true, 8>(m) : short_m<F, false, 8>(m);
+    }
     if (L == 16) return xf ? short_m<F, true, 16>(m) : short_m<F, false, 16>(m);
     return xf ? short_m<F, true, 32>(m) : short_m<F, false, 32>(m);
 }
 
 // Rows a wave of the short form for nb blocks a row.
-inline uint32_t short_rows(uint32_t nb, uint32_t bb) {
+inline uint32_t short_rows(uint32_t nb, uint32_t block, uint32_t bb, uint32_t m) {
     const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
     const uint32_t rows = (64 / L) * short_np(L);
+    if (L == 8 && block == 128 && m <= 2 && 32 * nb * bb <= 2 * kShortBytes) return 32u;  // short_l8_wide
     return rows * nb * bb > kShortBytes ? 4u : rows;  // the 2-pass form of short_pick
 }
 
@@ -403,7 +418,8 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     default: sk = short_pick<6>(a->m, xf, nb); break;
     }
     if (sk) {
-        const uint32_t rows = short_rows(nb, block_shape(a->w_dtype).bytes);
+        const BlockShape bs = block_shape(a->w_dtype);
+        const uint32_t rows = short_rows(nb, bs.block, bs.bytes, a->m);
         const uint32_t waves = (a->n + rows - 1) / rows;
         hipLaunchKernelGGL(sk, dim3((waves + kWaves - 1) / kWaves), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
         TS_CHECK_LAUNCH("lanes (block form, short rows) launch");

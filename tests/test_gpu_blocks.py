@@ -37,7 +37,7 @@ def _dev(wb):
 
 
 @pytest.mark.parametrize("form", FORMS)
-@pytest.mark.parametrize("m,n,k", [(1, 2048, 1024), (2, 300, 3072), (1, 37, 4096), (3, 37, 8192), (3, 37, 1024), (4, 1024, 512),
+@pytest.mark.parametrize("m,n,k", [(1, 2048, 1024), (2, 300, 3072), (2, 100, 1024), (1, 37, 4096), (3, 37, 8192), (3, 37, 1024), (4, 1024, 512),
                                    (1, 151936, 1024)])
 def test_block_product_bit_exact(form, m, n, k):
     from tessera_amd import rules as R
