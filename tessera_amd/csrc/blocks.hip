@@ -32,6 +32,7 @@ struct BlockParams {
     uint32_t m, n, k;
     uint32_t stages;
     int out_bf16;
+    uint32_t wide;  // short form: rows of whole 16-byte chunks, 16-byte aligned (16-byte loads)
 };
 
 // Blocks per LDS slice: one per lane (a 128-code block's part is one ordered sum, so
@@ -196,7 +197,9 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     constexpr int G = 64 / L, RT = G * NP;
     static_assert(RT * M <= 64, "one lane an output");
     // One word past the rows: the aligned word reads of the last block's codes.
-    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][SBYTES / 4 + 4];
+    // Whole KiB (the loads' last instruction fills its KiB) and one word more: the
+    // aligned word reads of the last block's codes.
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][(SBYTES + 1023) / 1024 * 256 + 4];
     __shared__ __attribute__((aligned(16))) float contrib[kWaves][RT * M][L];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -207,9 +210,17 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     const uint32_t words = nrows * (nb * BB / 4);
     const uint32_t *src = (const uint32_t *)(p.w + BF::HEAD + (size_t)r0 * nb * BB);
     char *base = (char *)stage[wave];
-    for (uint32_t w0 = 0; w0 < words; w0 += 64) {
-        const uint32_t i = min(w0 + lane, words - 1);  // past the end: a repeat, unused
-        __builtin_amdgcn_global_load_lds((const void *)(src + i), (block_lds_void *)(base + 4 * w0), 4, 0, 0);
+    if (p.wide) {  // 16-byte chunks (lane i of an instruction at 16 i)
+        const uint32_t chunks = words / 4;
+        for (uint32_t c0 = 0; c0 < chunks; c0 += 64) {
+            const uint32_t i = min(c0 + lane, chunks - 1);  // past the end: a repeat, unused
+            __builtin_amdgcn_global_load_lds((const void *)(src + 4 * i), (block_lds_void *)(base + 16 * c0), 16, 0, 0);
+        }
+    } else {
+        for (uint32_t w0 = 0; w0 < words; w0 += 64) {
+            const uint32_t i = min(w0 + lane, words - 1);  // past the end: a repeat, unused
+            __builtin_amdgcn_global_load_lds((const void *)(src + i), (block_lds_void *)(base + 4 * w0), 4, 0, 0);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_wave_barrier();
@@ -405,6 +416,10 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     BlockParams p;
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
+    {
+        const BlockShape bs = block_shape(a->w_dtype);
+        p.wide = (a->k / bs.block) * bs.bytes % 16 == 0 && aligned((const uint8_t *)a->w + bs.head, 16);
+    }
     const bool xf = a->x_dtype == TS_F32;
     const uint32_t nb = a->k / block_shape(a->w_dtype).block;
     ShortKern sk = nullptr;
