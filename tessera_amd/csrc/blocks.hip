@@ -14,7 +14,8 @@
 // from 0.0 in j order, no contraction), times the block scale; lane (row, m) then adds
 // the contributions of activation row m in block order, and the head (nvfp4) scales
 // the total. Every rounding step is the reference's, so the product is bit-identical
-// to Block::dot for the same f32 activations.
+// to Block::dot for the same f32 activations. Rows of at most 32 blocks take the short
+// form (block_gemv_short_kernel below): lanes over (row, block) pairs instead.
 #include "blockform.h"
 
 namespace ts {
@@ -174,20 +175,21 @@ typedef __attribute__((address_space(3))) void block_lds_void;
 template <int T>
 TS_DEV ts_f32x2_t fp4_pair(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, T); }
 
-constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; + 16 of pad: 9 KiB)
+constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; staged in 9 KiB + a word)
 
-// Rows a pass and passes a wave of the short form with L lanes a row: 16 rows a wave
-// (8 at L = 32, so the rows' bytes fit kShortBytes).
+// Passes a wave of the short form with L lanes a row (64 / L rows a pass): 16 rows a
+// wave, 8 at L = 32, so the rows' bytes fit kShortBytes. short_pick also takes 2 passes
+// at L = 32 for rows too wide for 4, and 4 passes at L = 8 for 128-code blocks.
 constexpr int short_np(int L) { return L == 32 ? 4 : L == 16 ? 4 : 2; }
 
 // Short rows (at most 32 blocks, e.g. 1024 codes of 32-code blocks, or of 128-code
 // ones): L lanes a row (nb <= L), 64 / L rows a pass, so every lane decodes a block
 // where the form above would leave 64 - nb lanes idle. A wave's NP passes (RT rows)
-// are contiguous bytes: they go straight to LDS (4-byte global_load_lds, lane i of an
-// instruction at 4 i: no staging registers); a lane then runs its NP blocks (same
-// block index, NP rows) as NP interleaved chains over one load of x. The arithmetic
-// per block and the block-order sum of each output are those of block_gemv_kernel,
-// so both give the same bits.
+// are contiguous bytes: they go straight to LDS (global_load_lds, 16 bytes a lane when
+// the rows are whole 16-byte chunks, else 4: no staging registers); a lane then runs
+// its NP blocks (same block index, NP rows) as NP interleaved chains over one load of
+// x. The arithmetic per block and the block-order sum of each output are those of
+// block_gemv_kernel, so both give the same bits.
 template <int F, int M, bool XF32, int L, int NP, uint32_t SBYTES = kShortBytes>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockParams p) {
 #pragma clang fp contract(off)
@@ -196,7 +198,6 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     constexpr int P = B < 32 ? B : 32;
     constexpr int G = 64 / L, RT = G * NP;
     static_assert(RT * M <= 64, "one lane an output");
-    // One word past the rows: the aligned word reads of the last block's codes.
     // Whole KiB (the loads' last instruction fills its KiB) and one word more: the
     // aligned word reads of the last block's codes.
     __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][(SBYTES + 1023) / 1024 * 256 + 4];
