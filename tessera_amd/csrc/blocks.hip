@@ -74,6 +74,65 @@ TS_DEV void load_x(const void *x, size_t at, float *xv) {
     }
 }
 
+// e2m1 codes of byte T of w (low nibble first) as f32 (scale 1: exact).
+template <int T>
+TS_DEV ts_f32x2_t fp4_pair(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, T); }
+
+// Codes q P .. q P + P - 1 of the block whose codes start at byte `at` of the LDS
+// words `w` (exact, before the scale), read as aligned words split by alignbyte
+// instead of byte reads; the word after the block's codes must be readable.
+template <int F, int P>
+TS_DEV void codes_from_words(const uint32_t *w, uint32_t at, int q, float *wv) {
+    using BF = BlockForm<F>;
+    if (BF::BITS == 8) {
+        const uint32_t off = at + q * P, w0 = off >> 2, sh = off & 3u;
+        uint32_t d[P / 4 + 1];
+#pragma unroll
+        for (int e = 0; e <= P / 4; e++) d[e] = w[w0 + e];
+#pragma unroll
+        for (int e = 0; e < P / 4; e++) {
+            const uint32_t v = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
+            if (BF::CODE == kCodeI8) {
+#pragma unroll
+                for (int t = 0; t < 4; t++) wv[4 * e + t] = (float)((int32_t)(v << (24 - 8 * t)) >> 24);
+            } else {
+                e4m3x4_float(v, wv + 4 * e);
+            }
+        }
+    } else {
+        // Byte i of a piece holds codes 2 i, 2 i + 1 (low nibble first), or i and
+        // i + B / 2 (q4_0's halves).
+        const uint32_t off = at + q * (P / 2), w0 = off >> 2, sh = off & 3u;
+        uint32_t d[P / 8 + 1];
+#pragma unroll
+        for (int e = 0; e <= P / 8; e++) d[e] = w[w0 + e];
+#pragma unroll
+        for (int e = 0; e < P / 8; e++) {
+            const uint32_t v = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int i = 4 * e + t;
+                if (BF::CODE == kCodeE2M1) {
+                    const ts_f32x2_t c = t == 0 ? fp4_pair<0>(v) : t == 1 ? fp4_pair<1>(v)
+                                       : t == 2 ? fp4_pair<2>(v) : fp4_pair<3>(v);
+                    wv[2 * i] = c[0];
+                    wv[2 * i + 1] = c[1];
+                } else {
+                    const float lo = (float)((v >> (8 * t)) & 15u) - 8.0f;
+                    const float hi = (float)((v >> (8 * t + 4)) & 15u) - 8.0f;
+                    if (BF::HALVES) {
+                        wv[i] = lo;
+                        wv[i + P / 2] = hi;
+                    } else {
+                        wv[2 * i] = lo;
+                        wv[2 * i + 1] = hi;
+                    }
+                }
+            }
+        }
+    }
+}
+
 template <int F, int M, bool XF32>
 __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) {
 #pragma clang fp contract(off)
@@ -82,7 +141,9 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
     constexpr int P = B < 32 ? B : 32;                   // elements decoded per piece
     constexpr int kSlice = CH * BB / 4;                  // words of one row's slice
     constexpr int kWords = (kSlice + 63) / 64;           // of them per lane
-    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kRows][kSlice];
+    // Each row's slice one word longer than its blocks: the aligned word reads of the
+    // last block's codes.
+    __shared__ __attribute__((aligned(16))) uint32_t stage[kWaves][kRows][kSlice + 4];
     __shared__ __attribute__((aligned(16))) float contrib[kWaves][kRows * M][CH];
 
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -128,9 +189,8 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
                     load_x<P, XF32>(p.x, (size_t)m * K + k0 + q * P, xv);
 #pragma unroll
                     for (int rr = 0; rr < kRows; rr++) {
-                        const uint8_t *codes = (const uint8_t *)stage[wave][rr] + lane * BB + SB;
                         float wv[P];
-                        block_codes<F, P>(codes, q, wv);
+                        codes_from_words<F, P>(stage[wave][rr], lane * BB + SB, q, wv);
 #pragma unroll
                         for (int j = 0; j < P; j++) part[rr] = part[rr] + xv[j] * wv[j];
                     }
@@ -170,10 +230,6 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
 }
 
 typedef __attribute__((address_space(3))) void block_lds_void;
-
-// e2m1 codes of byte T of w (low nibble first) as f32 (scale 1: exact).
-template <int T>
-TS_DEV ts_f32x2_t fp4_pair(uint32_t w) { return __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, T); }
 
 constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; staged in 9 KiB + a word)
 
@@ -244,56 +300,7 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
                 for (int i = 0; i < NP; i++) {
                     const uint32_t rr = min(i * G + g, nrows - 1);  // rows past the end: unused
                     float wv[P];
-                    if (BF::BITS == 8) {
-                        // Byte codes from aligned LDS words: words d[0..P/4] around them,
-                        // each 4 codes one alignbyte, then 4 converts (no byte reads).
-                        const uint32_t off = (rr * nb + b) * BB + SB + q * P, w0 = off >> 2, sh = off & 3u;
-                        uint32_t d[P / 4 + 1];
-#pragma unroll
-                        for (int e = 0; e <= P / 4; e++) d[e] = stage[wave][w0 + e];
-#pragma unroll
-                        for (int e = 0; e < P / 4; e++) {
-                            const uint32_t w = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
-                            if (BF::CODE == kCodeI8) {
-#pragma unroll
-                                for (int t = 0; t < 4; t++) wv[4 * e + t] = (float)((int32_t)(w << (24 - 8 * t)) >> 24);
-                            } else {
-                                e4m3x4_float(w, wv + 4 * e);
-                            }
-                        }
-                    } else {
-                        // Nibble codes the same way: P / 2 bytes in aligned words, byte i
-                        // holding codes 2 i, 2 i + 1 (low nibble first), or i and i + B / 2
-                        // (q4_0's halves).
-                        const uint32_t off = (rr * nb + b) * BB + SB + q * (P / 2), w0 = off >> 2, sh = off & 3u;
-                        uint32_t d[P / 8 + 1];
-#pragma unroll
-                        for (int e = 0; e <= P / 8; e++) d[e] = stage[wave][w0 + e];
-#pragma unroll
-                        for (int e = 0; e < P / 8; e++) {
-                            const uint32_t w = __builtin_amdgcn_alignbyte(d[e + 1], d[e], sh);
-#pragma unroll
-                            for (int t = 0; t < 4; t++) {
-                                const int i = 4 * e + t;  // byte of the piece
-                                if (BF::CODE == kCodeE2M1) {
-                                    const ts_f32x2_t v = t == 0 ? fp4_pair<0>(w) : t == 1 ? fp4_pair<1>(w)
-                                                       : t == 2 ? fp4_pair<2>(w) : fp4_pair<3>(w);
-                                    wv[2 * i] = v[0];
-                                    wv[2 * i + 1] = v[1];
-                                } else {
-                                    const float lo = (float)((w >> (8 * t)) & 15u) - 8.0f;
-                                    const float hi = (float)((w >> (8 * t + 4)) & 15u) - 8.0f;
-                                    if (BF::HALVES) {
-                                        wv[i] = lo;
-                                        wv[i + P / 2] = hi;
-                                    } else {
-                                        wv[2 * i] = lo;
-                                        wv[2 * i + 1] = hi;
-                                    }
-                                }
-                            }
-                        }
-                    }
+                    codes_from_words<F, P>(stage[wave], (rr * nb + b) * BB + SB, q, wv);
 #pragma unroll
                     for (int j = 0; j < P; j++) part[i] = part[i] + xv[j] * wv[j];
                 }
