@@ -344,34 +344,32 @@ ShortKern short_l8_wide(uint32_t m) {
                   : block_gemv_short_kernel<F, 2, XF32, 8, 4, 2 * kShortBytes>;
 }
 
-// The short form for nb <= 32 blocks a row whose wave rows fit kShortBytes, or NULL.
+// The short form for nb <= 32 blocks a row whose wave rows fit its stage, or NULL;
+// *rows: the rows a wave of it takes.
 template <int F>
-ShortKern short_pick(uint32_t m, bool xf, uint32_t nb) {
+ShortKern short_pick(uint32_t m, bool xf, uint32_t nb, uint32_t *rows) {
+    using BF = BlockForm<F>;
     const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
     if (nb > 32) return nullptr;
-    if ((uint64_t)(64 / L) * short_np(L) * nb * BlockForm<F>::BB > kShortBytes) {
+    *rows = (64 / L) * short_np(L);
+    if ((uint64_t)*rows * nb * BF::BB > kShortBytes) {
         // Wide blocks (128 codes): 2 passes of 2 rows at L = 32 (4 rows a wave).
-        if (L == 32 && (uint64_t)2 * 2 * nb * BlockForm<F>::BB <= kShortBytes)
+        *rows = 4;
+        if (L == 32 && (uint64_t)4 * nb * BF::BB <= kShortBytes)
             return xf ? short_m<F, true, 32, 2>(m) : short_m<F, false, 32, 2>(m);
         return nullptr;
     }
     if (L == 8) {
         // 128-code blocks: 4 passes of 8 rows (a wave's 32 rows in 17 KiB, two groups a
         // CU) instead of 2.
-        if (BlockForm<F>::B == 128 && m <= 2 && (uint64_t)32 * nb * BlockForm<F>::BB <= 2 * kShortBytes)
+        if (BF::B == 128 && m <= 2 && (uint64_t)32 * nb * BF::BB <= 2 * kShortBytes) {
+            *rows = 32;
             return xf ? short_l8_wide<F, true>(m) : short_l8_wide<F, false>(m);
+        }
         return xf ? short_m<F, true, 8>(m) : short_m<F, false, 8>(m);
     }
     if (L == 16) return xf ? short_m<F, true, 16>(m) : short_m<F, false, 16>(m);
     return xf ? short_m<F, true, 32>(m) : short_m<F, false, 32>(m);
-}
-
-// Rows a wave of the short form for nb blocks a row.
-inline uint32_t short_rows(uint32_t nb, uint32_t block, uint32_t bb, uint32_t m) {
-    const int L = nb <= 8 ? 8 : nb <= 16 ? 16 : 32;
-    const uint32_t rows = (64 / L) * short_np(L);
-    if (L == 8 && block == 128 && m <= 2 && 32 * nb * bb <= 2 * kShortBytes) return 32u;  // short_l8_wide
-    return rows * nb * bb > kShortBytes ? 4u : rows;  // the 2-pass form of short_pick
 }
 
 using Kern = void (*)(BlockParams);
@@ -431,18 +429,17 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     const bool xf = a->x_dtype == TS_F32;
     const uint32_t nb = a->k / block_shape(a->w_dtype).block;
     ShortKern sk = nullptr;
+    uint32_t rows = 0;
     switch (a->w_dtype) {
-    case TS_Q8_0: sk = short_pick<0>(a->m, xf, nb); break;
-    case TS_MXFP8: sk = short_pick<1>(a->m, xf, nb); break;
-    case TS_INT4_G32: sk = short_pick<2>(a->m, xf, nb); break;
-    case TS_Q4_0: sk = short_pick<3>(a->m, xf, nb); break;
-    case TS_NVFP4: sk = short_pick<4>(a->m, xf, nb); break;
-    case TS_MXFP4: sk = short_pick<5>(a->m, xf, nb); break;
-    default: sk = short_pick<6>(a->m, xf, nb); break;
+    case TS_Q8_0: sk = short_pick<0>(a->m, xf, nb, &rows); break;
+    case TS_MXFP8: sk = short_pick<1>(a->m, xf, nb, &rows); break;
+    case TS_INT4_G32: sk = short_pick<2>(a->m, xf, nb, &rows); break;
+    case TS_Q4_0: sk = short_pick<3>(a->m, xf, nb, &rows); break;
+    case TS_NVFP4: sk = short_pick<4>(a->m, xf, nb, &rows); break;
+    case TS_MXFP4: sk = short_pick<5>(a->m, xf, nb, &rows); break;
+    default: sk = short_pick<6>(a->m, xf, nb, &rows); break;
     }
     if (sk) {
-        const BlockShape bs = block_shape(a->w_dtype);
-        const uint32_t rows = short_rows(nb, bs.block, bs.bytes, a->m);
         const uint32_t waves = (a->n + rows - 1) / rows;
         hipLaunchKernelGGL(sk, dim3((waves + kWaves - 1) / kWaves), dim3(kWaves * 64), 0, (hipStream_t)stream, p);
         TS_CHECK_LAUNCH("lanes (block form, short rows) launch");
