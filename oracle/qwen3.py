@@ -34,6 +34,17 @@ class Qwen3:
         self.kv = [dict(k=np.zeros((c["max_context"], c["kv_heads"], c["head_dim"]), np.float32),
                         v=np.zeros((c["max_context"], c["kv_heads"], c["head_dim"]), np.float32))
                    for _ in range(c["layers"])]
+        # Kept rows below `origin` are not part of the slot (0: the slot starts at position 0).
+        # Rotations use the absolute positions; attention reads keys origin..pos.
+        self.origin = 0
+        # Format of the kept rows: bf16, as the device stores them.
+        self.keep = O.bf16_round
+
+    def norm_rope(self, t, gain, positions):
+        """Per-head RmsNorm, then Halves RoPE at the rows' positions
+        (engine/models/src/shared.rs:109-145: q_norm/k_norm precede the rotation)."""
+        c = self.c
+        return O.rope(O.rms_norm(t, gain, c["eps"]), positions, c["theta"], "halves")
 
     def forward(self, tokens, positions) -> np.ndarray:
         """Rows of one slot at `positions`; returns the last row's logits."""
@@ -51,13 +62,14 @@ class Qwen3:
             q = qkv[:, : Hq * D].reshape(rows, Hq, D)
             k = qkv[:, Hq * D:(Hq + Hkv) * D].reshape(rows, Hkv, D)
             v = qkv[:, (Hq + Hkv) * D:].reshape(rows, Hkv, D)
-            q = O.rope(O.rms_norm(q, L["q_norm"], eps), positions, theta, "halves")
-            k = O.rope(O.rms_norm(k, L["k_norm"], eps), positions, theta, "halves")
+            q = self.norm_rope(q, L["q_norm"], positions)
+            k = self.norm_rope(k, L["k_norm"], positions)
             kv = self.kv[li]
-            kv["k"][positions] = O.bf16_round(k)                            # Append (bf16 kept rows)
-            kv["v"][positions] = O.bf16_round(v)
-            attn = O.attend_rows(q, kv["k"], kv["v"], np.zeros(rows, np.uint32), positions,
-                                 c["max_context"], scale)                   # attend_rows, causal
+            kv["k"][positions] = self.keep(k)                            # Append (bf16 kept rows)
+            kv["v"][positions] = self.keep(v)
+            o0 = self.origin                                                # first kept row of the slot
+            attn = O.attend_rows(q, kv["k"][o0:], kv["v"][o0:], np.zeros(rows, np.uint32), positions - o0,
+                                 c["max_context"] - o0, scale)              # attend_rows, causal
             x = O.product_bf16w(attn.reshape(rows, Hq * D), L["o"]) + x    # o, then .add(x)
             h = O.rms_norm(x, L["ln2"], eps)
             gu = O.product_bf16w(h, L["gate_up"])

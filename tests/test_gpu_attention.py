@@ -324,3 +324,30 @@ def test_refused_beyond_max_position():
     torch.cuda.synchronize()
     assert int(status.item()) == abi.TS_STATUS_POSITION
     assert np.all(np.isnan(got))
+
+
+def test_prefill_c3_full():
+    """The whole C3 prefill shape as benchmarked: 4 slots x 2048 causal rows (8192 rows
+    packed back to back), bf16 q, 16 q / 8 kv heads, shuffled 16-row pages, one
+    launch; the oracle on 24 sampled rows of each slot (first and last positions, the
+    page and 128-row group edges, random ones). Tolerance as the bf16-q case: 4e-3."""
+    from tessera_amd import rules as R
+    lens = [2048] * 4
+    slots = np.repeat(np.arange(4), 2048).astype(np.uint32)
+    positions = np.tile(np.arange(2048), 4).astype(np.uint32)
+    c = paged_case(3, lens, pos=(slots, positions))
+    qb = O.bf16_narrow(c["q"])
+    s = 1 / math.sqrt(128)
+    got = from_dev(R.flash_rows(to_dev(qb, torch), to_dev(c["kb"], torch), to_dev(c["vb"], torch),
+                                to_dev(c["slots"], torch, torch.int32), to_dev(c["positions"], torch, torch.int32),
+                                keys=c["keys"], scale=s, table=to_dev(c["table"], torch, torch.int32),
+                                kept_pages=c["kept_pages"], page=c["page"]))
+    r = rng(33)
+    pick = []
+    for sl in range(4):
+        base = sl * 2048
+        fixed = [0, 1, 15, 16, 127, 128, 1023, 1024, 2046, 2047]
+        pick += [base + p for p in fixed] + list(base + r.choice(2048, 14, replace=False))
+    pick = np.array(sorted(set(pick)))
+    sub = dict(c, q=O.bf16_widen(qb[pick]), slots=c["slots"][pick], positions=c["positions"][pick])
+    np.testing.assert_allclose(got[pick], want(sub, s), atol=4e-3, rtol=0)

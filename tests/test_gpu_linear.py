@@ -50,7 +50,7 @@ def test_linear_f32_rows_bf16_weights(m, n, k):
 
 
 @pytest.mark.parametrize("m", [1, 4, 16, 128])
-@pytest.mark.parametrize("k,n", [(1024, 2048), (2048, 1024), (3072, 1024)])
+@pytest.mark.parametrize("k,n", [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 6144), (3072, 1024)])
 def test_linear_bf16_sweep_shapes(m, k, n):
     """C2: N(0,1) bf16 x and w, f32 accumulate, bf16 and f32 out."""
     R = _rules()
@@ -62,6 +62,34 @@ def test_linear_bf16_sweep_shapes(m, k, n):
     _check(got, want, _bound(xf, wf))
     got16 = from_dev(R.linear(to_dev(xb, torch), to_dev(wb, torch), out_dtype=torch.bfloat16))
     assert max_rel(got16, want) <= 2e-2
+
+
+@pytest.fixture(scope="module")
+def lm_head_case():
+    r = rng(2153)
+    k, n = 1024, 151936
+    wb = O.bf16_narrow(r.standard_normal((n, k)).astype(np.float32))
+    return wb, to_dev(wb, torch)
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 128])
+def test_linear_bf16_sweep_lm_head(m, lm_head_case):
+    """C2 lm_head 1024 x 151936 at the few-row sizes, bf16 x and w: the whole product
+    launched as benchmarked, f32 and bf16 out, checked on column slices (first,
+    middle, the ragged end) against the oracle."""
+    R = _rules()
+    wb, wd = lm_head_case
+    n = wb.shape[0]
+    r = rng(2154 + m)
+    xb, xf = bf16_bits_normal(r, (m, 1024))
+    xd = to_dev(xb, torch)
+    got32 = R.linear(xd, wd)
+    got16 = R.linear(xd, wd, out_dtype=torch.bfloat16)
+    for lo, hi in [(0, 700), (75000, 75500), (n - 600, n)]:
+        w = np.ascontiguousarray(wb[lo:hi])
+        want = O.product_bf16w(xf, w)
+        _check(from_dev(got32[:, lo:hi].contiguous()), want, _bound(xf, O.bf16_widen(w)))
+        assert max_rel(from_dev(got16[:, lo:hi].contiguous()), want) <= 2e-2
 
 
 @pytest.mark.parametrize("m,n,k", [(2048, 8192, 256), (2000, 7777, 192), (2000, 7777, 136), (1300, 12300, 64),

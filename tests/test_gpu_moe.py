@@ -178,3 +178,64 @@ def test_moe_layer_matches_oracle(tokens, hidden, experts, top, ffn):
     s_inner = O.act("silu", s_gu[:, :ffn]) * s_gu[:, ffn:]
     want = want + O.product_bf16w(s_inner, sout_b)
     assert max_rel(from_dev(y), want) <= 2e-2
+
+
+def test_moe_layer_c5_full_shape():
+    """C5 as benchmarked: 4096 tokens, hidden 4096, 128 experts top-8, FFN 1536, one
+    shared expert, the gate logits given as scores (N(0,1) f32, seed 3) and the weights
+    drawn as the bench draws them. Routing ids bit-exact on every row against the
+    oracle's top_k; the stable sort's permutation (read from the routing workspace of
+    a picked launch with the same ids) bit-exact against a stable argsort by expert;
+    gates within 2e-6; the layer's output within max-rel 2e-2 of the oracle on 64
+    sampled tokens, which together pick at least 100 experts."""
+    R = _rules()
+    O.set_threads(O.lib().or_threads_available())
+    tokens, hidden, experts, top, ffn = 4096, 4096, 128, 8, 1536
+    g = torch.Generator(device="cuda").manual_seed(3)
+    logits = torch.randn((tokens, experts), device="cuda", generator=g)
+    h = torch.randn((tokens, hidden), device="cuda", generator=g).to(torch.bfloat16)
+    w_in = torch.empty((experts, 2 * ffn, hidden), device="cuda", dtype=torch.bfloat16)
+    w_out = torch.empty((experts, hidden, ffn), device="cuda", dtype=torch.bfloat16)
+    for e in range(experts):
+        w_in[e] = (torch.randn((2 * ffn, hidden), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        w_out[e] = (torch.randn((hidden, ffn), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    s_in = (torch.randn((2 * ffn, hidden), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    s_out = (torch.randn((hidden, ffn), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    print("C5 full shape", flush=True)
+    y, ids, gates = R.moe_layer(h, None, w_in, w_out, top=top, shared_in=s_in, shared_out=s_out, scores=logits)
+    torch.cuda.synchronize()
+    scores = from_dev(logits)
+    ids_np = from_dev(ids).astype(np.uint32)
+    assert np.array_equal(ids_np, O.top_k(scores, top))
+    want_gates = O.softmax(O.take(scores, ids_np))
+    assert np.max(np.abs(from_dev(gates) - want_gates)) <= 2e-6
+    # the permutation: a picked launch over the same ids leaves its routing in the workspace
+    flat = ids_np.reshape(-1)
+    R.picked(h, w_in, ids, n=16, repeat=top)
+    torch.cuda.synchronize()
+    words = R.workspace(h.device).buf.view(torch.int32).cpu().numpy().view(np.uint32)
+    rows, B = flat.size, experts + 1
+    chunks = (rows + 255) // 256
+    row_start = words[chunks * B: chunks * B + B + 1]
+    perm = words[chunks * B + (B + 1) + (experts + 1):][:rows]
+    assert np.array_equal(perm, np.argsort(flat, kind="stable").astype(np.uint32))
+    assert np.array_equal(row_start[:B], np.searchsorted(np.sort(flat), np.arange(B)).astype(np.uint32))
+    assert row_start[B] == rows
+    # the output on sampled tokens, through the oracle with the same picks
+    sample = np.sort(rng(64).choice(tokens, 64, replace=False))
+    assert len(set(ids_np[sample].reshape(-1).tolist())) >= 100
+    hb = h.view(torch.int16).cpu().numpy().view(np.uint16)[sample]
+    hx = O.bf16_widen(hb)
+    bits = lambda t: t.view(torch.int16).cpu().numpy().view(np.uint16)
+    want = np.zeros((len(sample), hidden), np.float32)
+    y_picks = np.zeros((len(sample), top, hidden), np.float32)
+    for e in np.unique(ids_np[sample]):
+        ti, pi = np.nonzero(ids_np[sample] == e)
+        gu = O.product_bf16w(hx[ti], bits(w_in[e]))
+        inner = O.act("silu", gu[:, :ffn]) * gu[:, ffn:]
+        y_picks[ti, pi] = O.product_bf16w(inner, bits(w_out[e]))
+    want = O.mix(y_picks, want_gates[sample])
+    s_gu = O.product_bf16w(hx, bits(s_in))
+    want = want + O.product_bf16w(O.act("silu", s_gu[:, :ffn]) * s_gu[:, ffn:], bits(s_out))
+    assert max_rel(from_dev(y)[sample], want) <= 2e-2
+    O.set_threads(1)

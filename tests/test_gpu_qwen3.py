@@ -141,3 +141,37 @@ def test_qwen3_c1_teacher_forced(step):
     with pytest.raises(Exception, match="past the vocabulary"):
         m.set_token(cfg.vocab)
     m.close()
+
+
+def test_qwen3_c1_steps_in_one_launch():
+    """The benchmarked mode at the C1 shape: 32 greedy steps in one persistent launch
+    give the tokens and, bit for bit, the final logits of 32 one-step launches (same
+    arithmetic; the in-launch token hand-off, the per-step epochs and the kept rows
+    appended inside the launch are what differ). The final logits are then held to the
+    oracle's forward over the same tokens at positions 128..159: cosine >= 0.999,
+    max-rel <= 2e-2, greedy token equal unless a near-tie."""
+    from tessera_amd.qwen3 import Qwen3, default_config
+    cfg = default_config()
+    prompt = np.random.default_rng(1).integers(0, cfg.vocab, 128).astype(np.uint32)
+    runs = []
+    for per_call in (32, 1):
+        m = Qwen3(cfg, seed=0)
+        assert m.step_mode
+        first = m.prefill(prompt)
+        toks = np.concatenate([m.decode(per_call) for _ in range(32 // per_call)])
+        runs.append((first, toks, m.logits(), m.position))
+        if per_call == 1:
+            ref_w = host_weights(m)
+        m.close()
+    (f0, t0, l0, p0), (f1, t1, l1, p1) = runs
+    assert f0 == f1 and p0 == p1 == 160
+    assert np.array_equal(t0, t1)
+    assert np.array_equal(l0, l1)
+    O.set_threads(O.lib().or_threads_available())
+    ref = OracleQwen3(ref_w)
+    ref.forward(prompt, np.arange(128))
+    fed = np.concatenate([[f0], t0[:-1]]).astype(np.uint32)     # step i reads the token step i-1 picked
+    want = ref.forward(fed, 128 + np.arange(32))
+    c, r = cosine(l0, want), max_rel(l0, want)
+    assert c >= 0.999 and r <= 2e-2, (c, r)
+    assert greedy_agrees(int(t0[-1]), want, 1e-3 * np.abs(want).max())

@@ -13,6 +13,9 @@ by cases whose answer does not go through the composition's own code:
   whatever the attention does;
 * a prompt prefilled in one call and the same prompt fed one token at a time give the
   same last logits (kept rows appended at their positions, causal masking).
+* RoPE after the per-head norm makes attention depend on relative positions only: the
+  same prompt placed at positions s..s+n-1 gives the logits of positions 0..n-1, which
+  fails for the rotation and the norm swapped or a row rotated by the wrong position.
 A dropped residual, a norm on the wrong tensor, a wrong GQA head map or a transposed
 product fails one of them.
 """
@@ -105,3 +108,62 @@ def test_prefill_equals_token_by_token():
     # And the last token does depend on the earlier ones (the causal rows are read).
     c = Qwen3(w).forward([toks[-1]], [0])
     assert not np.allclose(a, c)
+
+
+class RopeFirst(Qwen3):
+    """The composition with the rotation and the per-head norm swapped (a plausible
+    mistake the shift test must catch)."""
+
+    def norm_rope(self, t, gain, positions):
+        c = self.c
+        return O.rms_norm(O.rope(t, positions, c["theta"], "halves"), gain, c["eps"])
+
+
+def shifted_logits(cls, w, toks, shift, keep=None):
+    m = cls(w)
+    m.origin = shift
+    if keep is not None:
+        m.keep = keep
+    return m.forward(toks, shift + np.arange(len(toks)))
+
+
+def test_rope_after_norm_is_shift_invariant():
+    """RoPE makes q.k depend on the positions' difference only, so the same prompt
+    placed at positions s..s+n-1 (the slot's keys starting at s) gives the logits of
+    positions 0..n-1 — up to the bf16 rounding of the kept k rows, whose rotated values
+    differ with the absolute position. This pins the q/k norm -> RoPE order and the
+    position each row is rotated by (engine/models/src/shared.rs:109-145) at positions
+    > 0, with non-uniform q_norm / k_norm gains (a norm after the rotation breaks the
+    invariance; so does a row rotated by the wrong position)."""
+    w = tiny(4)
+    for L in w.layers:
+        L["q_norm"] = (1.0 + 0.5 * np.random.default_rng(5).standard_normal(L["q_norm"].size)).astype(np.float32)
+        L["k_norm"] = (1.0 + 0.5 * np.random.default_rng(6).standard_normal(L["k_norm"].size)).astype(np.float32)
+    w.cfg["max_context"] = 64
+    toks = [4, 9, 33, 1, 17, 26, 8]
+    exact = lambda a: a
+    base = shifted_logits(Qwen3, w, toks, 0, exact)
+    scale = np.abs(base).max()
+    for s in (1, 13, 40):
+        # f32 kept rows: equal up to f32 rounding of the rotations
+        d = np.abs(shifted_logits(Qwen3, w, toks, s, exact) - base).max() / scale
+        assert d <= 1e-5, (s, d)
+        # bf16 kept rows (the device's format): the rounding of rotated k moves with s
+        b16 = shifted_logits(Qwen3, w, toks, 0)
+        d = np.abs(shifted_logits(Qwen3, w, toks, s) - b16).max() / np.abs(b16).max()
+        assert d <= 2e-2, (s, d)
+    # The swapped composition is not invariant: it moves by far more than either bound.
+    rb = shifted_logits(RopeFirst, w, toks, 0, exact)
+    for s in (1, 13, 40):
+        d = np.abs(shifted_logits(RopeFirst, w, toks, s, exact) - rb).max() / np.abs(rb).max()
+        assert d > 0.1, (s, d)
+
+    class OffByOne(Qwen3):
+        """q of the last row rotated one position too far."""
+
+        def norm_rope(self, t, gain, positions):
+            last = (np.arange(len(positions)) == len(positions) - 1) & (t.shape[1] == self.c["heads"])
+            return super().norm_rope(t, gain, positions + last.astype(np.uint32))
+
+    ob = shifted_logits(OffByOne, w, toks, 0, exact)
+    assert np.abs(ob - base).max() / scale > 1e-2
