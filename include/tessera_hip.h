@@ -57,8 +57,42 @@ enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 =
                                  greedy pick folded into workspace key[m] (uint64; zero before
                                  the launch): tessera_hip_argmax_keys reads and clears them */
 
+/* A general chain of elementwise stages, run on a product's sum before its store or
+ * over an input by tessera_hip_map (engine/plan/lower/src/kernels/map.rs:40-59 MapStage,
+ * applied at the store by `finish`, map.rs:155-185; the Finished site,
+ * engine/plan/lower/src/sites/matmul.rs:117-200). The chain reads 1 + (its Add and Mul
+ * stages) values: read 0 starts v, and each Add / Mul stage reads the next one. Read
+ * `sum` is the product's sum (tessera_hip_map: its input x); the others are
+ * operand[0], operand[1], ... in order. Each stage is one f32 operation rounded on its
+ * own (no fused multiply-add), as the interpreter evaluates Stage::Add / Mul / Scale /
+ * Act (engine/ir/interp/src/cpu.rs:8-29,353-390):
+ *   TS_MAP_ADD    v = v + next read        TS_MAP_SCALE  v = v * by
+ *   TS_MAP_MUL    v = v * next read        TS_MAP_ACT    v = act(v), act = TS_ACT_*
+ * Activations (cpu.rs:8-29): GeluTanh 0.5 x (1 + tanh(0.7978846 (x + 0.044715 x^3))),
+ * Silu x / (1 + e^-x), Sigmoid 1 / (1 + e^-x), Relu max(x, 0), Softplus
+ * max(x, 0) + log1p(e^-|x|), Exp e^x, Tanh tanh x. */
+#define TS_MAP_STAGES 8
+#define TS_MAP_OPERANDS 4
+enum { TS_MAP_ADD = 0, TS_MAP_MUL = 1, TS_MAP_SCALE = 2, TS_MAP_ACT = 3 };
+enum { TS_ACT_GELU_TANH = 0, TS_ACT_SILU = 1, TS_ACT_SIGMOID = 2, TS_ACT_RELU = 3, TS_ACT_SOFTPLUS = 4,
+       TS_ACT_EXP = 5, TS_ACT_TANH = 6 };
+typedef struct {
+    int32_t op;   /* TS_MAP_* */
+    int32_t act;  /* TS_ACT_*, TS_MAP_ACT only */
+    float by;     /* TS_MAP_SCALE only */
+} ts_map_stage;
+typedef struct {
+    const float *operand[TS_MAP_OPERANDS]; /* f32, as long as the output (a product's [m, n]) */
+    uint32_t spans[TS_MAP_OPERANDS];       /* tessera_hip_map only: 0 = as long as x; s > 0: operand j
+                                              is read at i % s (1: a scalar). Products need 0 (the
+                                              Finished site refuses repeating operands) */
+    uint32_t count;                        /* stages, <= TS_MAP_STAGES */
+    uint32_t sum;                          /* which read is the sum (or x), <= operands */
+    ts_map_stage stage[TS_MAP_STAGES];
+} ts_after;
+
 /* Version of this ABI; bumped on any struct layout change. */
-#define TS_ABI_VERSION 3
+#define TS_ABI_VERSION 4
 
 /* Checks that the current device is gfx950 and records its properties.
  * Replaces: the platform probe of engine/gpu/gpukit/src/rocm/context.rs:60-106
@@ -91,6 +125,8 @@ typedef struct {
     int32_t x_dtype, w_dtype, out_dtype;
     uint32_t stages;      /* TS_AFTER_* | TS_BEFORE_* bits */
     float eps;            /* RmsNorm epsilon */
+    const ts_after *after; /* host struct or NULL: a stage chain on the sum (after the SiLU pair
+                              when TS_AFTER_SILU_MUL is set); not with TS_AFTER_ADD / ARGMAX */
 } ts_linear_args;
 
 /* Picks `lanes` for m <= 64 and `tiled` otherwise (the cost select of
@@ -142,6 +178,8 @@ typedef struct {
     uint32_t first;       /* id of this set's first matrix */
     int32_t x_dtype, w_dtype, out_dtype;
     uint32_t stages;      /* 0 or TS_AFTER_SILU_MUL */
+    const ts_after *after; /* host struct or NULL: a stage chain on each output (operands
+                              [rows, n], indexed as out) */
 } ts_picked_args;
 
 /* Replaces: rule "picked" (engine/rules/linear/src/picked.rs:28-60,106-122) on the
@@ -235,6 +273,22 @@ int tessera_hip_attend_step(const ts_step_args *a, void *stream);
  * Replaces: rule "flash" / flash_rows (engine/rules/attention/src/flash.rs:416-503,
  * 506-591, 595-807). */
 int tessera_hip_flash_rows(const ts_rows_args *a, void *stream);
+
+/* ----------------------------------------------------------------------------
+ * Elementwise chains not fused into a product.
+ * out[i] = chain(x[i], operands at i) for i < len, with `after` as above (read
+ * `after.sum` is x; operands with spans repeat). out may alias x or an operand.
+ * Replaces: rule "map" / kernel Map (engine/plan/lower/src/kernels/map.rs:60-65,
+ * 187-260), e.g. the q pre-scale Map Scale(1/sqrt(d)) of
+ * engine/rules/attention/src/lib.rs:22-31.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const float *x;   /* [len] */
+    float *out;       /* [len] */
+    uint32_t len;
+    ts_after after;   /* by value */
+} ts_map_args;
+int tessera_hip_map(const ts_map_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------
  * Row stages and indices. Each takes one argument struct, fields in the reference

@@ -219,6 +219,40 @@ def act(kind: str, x) -> np.ndarray:
     return out
 
 
+def chain(total, stages, operands=(), sum_at: int = 0, spans=None) -> np.ndarray:
+    """A stage chain on `total` (a product's sum, or map's input): v = read 0, then each
+    stage in order, each read operand `Add`/`Mul` the next one (kernels/map.rs:125-185
+    stage_stmts / finish: read `sum_at` is `total`, the others the operands in order),
+    every operation one f32 rounding as interp's Stage::Add/Mul/Scale/Act
+    (cpu.rs:353-390; an operand with span s repeats, read at i % s, cpu.rs:362-366).
+    stages: "add", "mul", ("scale", by), or an activation name."""
+    total = _f32(total)
+    flat = total.reshape(-1)
+    n = flat.size
+    spans = list(spans or [0] * len(operands))
+
+    def read(i):
+        if i == sum_at:
+            return flat
+        j = i if i < sum_at else i - 1
+        o = _f32(operands[j]).reshape(-1)
+        return o[np.arange(n) % spans[j]] if spans[j] else o
+
+    v = read(0).copy()
+    nxt = 1
+    for st in stages:
+        if st in ("add", "mul"):
+            x = read(nxt)
+            nxt += 1
+            v = (v + x) if st == "add" else (v * x)
+        elif isinstance(st, tuple) and st[0] == "scale":
+            v = v * np.float32(st[1])
+        else:
+            v = act(st, v)
+        v = v.astype(np.float32)
+    return v.reshape(total.shape)
+
+
 def softmax(x) -> np.ndarray:
     out = _f32(x).copy()
     w = out.shape[-1]

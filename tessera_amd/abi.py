@@ -33,6 +33,27 @@ TS_AFTER_ARGMAX = 8
 
 U32_MAX = 0xFFFFFFFF
 
+# Stage chains (ts_after): stage ops and activations.
+TS_MAP_STAGES, TS_MAP_OPERANDS = 8, 4
+TS_MAP_ADD, TS_MAP_MUL, TS_MAP_SCALE, TS_MAP_ACT = 0, 1, 2, 3
+ACTS = {"gelu_tanh": 0, "silu": 1, "sigmoid": 2, "relu": 3, "softplus": 4, "exp": 5, "tanh": 6}
+
+
+class MapStage(C.Structure):
+    """ts_map_stage (include/tessera_hip.h)."""
+    _fields_ = [("op", C.c_int32), ("act", C.c_int32), ("by", C.c_float)]
+
+
+class After(C.Structure):
+    """ts_after (include/tessera_hip.h): a stage chain and its operands."""
+    _fields_ = [("operand", C.c_void_p * TS_MAP_OPERANDS), ("spans", C.c_uint32 * TS_MAP_OPERANDS),
+                ("count", C.c_uint32), ("sum", C.c_uint32), ("stage", MapStage * TS_MAP_STAGES)]
+
+
+class MapArgs(C.Structure):
+    """ts_map_args (include/tessera_hip.h)."""
+    _fields_ = [("x", C.c_void_p), ("out", C.c_void_p), ("len", C.c_uint32), ("after", After)]
+
 
 class LinearArgs(C.Structure):
     """ts_linear_args (include/tessera_hip.h)."""
@@ -42,7 +63,7 @@ class LinearArgs(C.Structure):
         ("workspace_bytes", C.c_size_t),
         ("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32),
         ("x_dtype", C.c_int32), ("w_dtype", C.c_int32), ("out_dtype", C.c_int32),
-        ("stages", C.c_uint32), ("eps", C.c_float),
+        ("stages", C.c_uint32), ("eps", C.c_float), ("after", C.c_void_p),
     ]
 
 
@@ -67,6 +88,7 @@ class PickedArgs(C.Structure):
         ("rows", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("count", C.c_uint32),
         ("stride", C.c_uint32), ("offset", C.c_uint32), ("repeat", C.c_uint32), ("first", C.c_uint32),
         ("x_dtype", C.c_int32), ("w_dtype", C.c_int32), ("out_dtype", C.c_int32), ("stages", C.c_uint32),
+        ("after", C.c_void_p),
     ]
 
 
@@ -144,6 +166,7 @@ SIGNATURES = {
     "tessera_hip_argmax_workspace": (C.c_size_t, [C.POINTER(ArgmaxArgs)]),
     "tessera_hip_argmax_keys": (C.c_int, [C.POINTER(KeysArgs), _P]),
     "tessera_hip_top_k": (C.c_int, [C.POINTER(TopKArgs), _P]),
+    "tessera_hip_map": (C.c_int, [C.POINTER(MapArgs), _P]),
 }
 
 

@@ -6,7 +6,7 @@
 // matrix is one tensor, so row r's blocks start at head + r (k / B) block bytes.
 #pragma once
 
-#include "common.h"
+#include "after.h"
 
 namespace ts {
 

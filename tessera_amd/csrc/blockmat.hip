@@ -37,6 +37,7 @@ struct MatParams {
     uint32_t m, n, k;
     uint32_t stages;
     int out_bf16;
+    ts_after after;  // stage chain (count 0: none)
 };
 
 template <int F>
@@ -229,29 +230,35 @@ __global__ __launch_bounds__(kThreads) void block_tiled_kernel(MatParams p) {
     // wn 32 + 16 j + 4 grp .. + 3 (SILU: gate j = 0, up j = 1, output columns
     // n0 + wn 16 + 4 grp .. + 3). nvfp4's head multiplies the sum (Block::dot).
     const float head = BF::HEAD ? *(const float *)p.w : 1.0f;
+    constexpr int JO = SILU ? 1 : 2;
+    // Value e = (i JO + j) 4 + r: row m0 + wm 32 + 16 i + col, column col_of(e).
+    auto row_of = [&](int e) { return m0 + wm * 32 + (uint32_t)(e / (4 * JO)) * 16 + col; };
+    auto col_of = [&](int e) {
+        return n0 + (SILU ? wn * 16 : wn * 32 + (uint32_t)(e / 4 % JO) * 16) + 4 * grp + (uint32_t)(e % 4);
+    };
+    float val[2 * JO * 4];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t m = m0 + wm * 32 + i * 16 + col;
-        if (m >= p.m) continue;
-#pragma unroll
-        for (int j = 0; j < (SILU ? 1 : 2); j++) {
-            const uint32_t n = n0 + (SILU ? wn * 16 : wn * 32 + j * 16) + 4 * grp;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                if (n + r >= N) break;
-                float v;
-                if (SILU) {
-                    const float g = head * acc[i][0][r], u = head * acc[i][1][r];
-                    v = g / (1.0f + expf(-g)) * u;
-                } else {
-                    v = head * acc[i][j][r];
-                }
-                const size_t at = (size_t)m * N + n + r;
-                if (p.stages & TS_AFTER_ADD) v += p.a0[at];
-                if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
-                else ((float *)p.out)[at] = v;
-            }
+    for (int e = 0; e < 2 * JO * 4; e++) {
+        const int i = e / (4 * JO), j = e / 4 % JO, r = e % 4;
+        if (SILU) {
+            const float g = head * acc[i][0][r], u = head * acc[i][1][r];
+            val[e] = g / (1.0f + expf(-g)) * u;
+        } else {
+            val[e] = head * acc[i][j][r];
         }
+    }
+    if (p.after.count)
+        after_values<2 * JO * 4, false>(p.after, val, [&](int e) { return (size_t)row_of(e) * N + col_of(e); },
+                                        [&](int e) { return row_of(e) < p.m && col_of(e) < N; });
+#pragma unroll
+    for (int e = 0; e < 2 * JO * 4; e++) {
+        const uint32_t m = row_of(e), n = col_of(e);
+        if (m >= p.m || n >= N) continue;
+        float v = val[e];
+        const size_t at = (size_t)m * N + n;
+        if (p.stages & TS_AFTER_ADD) v += p.a0[at];
+        if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
+        else ((float *)p.out)[at] = v;
     }
 }
 
@@ -279,6 +286,8 @@ int block_tiled_launch(const ts_linear_args *a, void *stream) {
     MatParams p;
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
+    const int rc = linear_after(a, "tiled (block form)", &p.after);
+    if (rc) return rc;
     Kern k;
     switch (a->w_dtype) {
     case TS_Q8_0: k = pick<0>(xf, silu); break;

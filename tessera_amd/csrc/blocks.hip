@@ -34,6 +34,7 @@ struct BlockParams {
     uint32_t stages;
     int out_bf16;
     uint32_t wide;  // short form: rows of whole 16-byte chunks, 16-byte aligned (16-byte loads)
+    ts_after after;  // stage chain (count 0: none)
 };
 
 // Blocks per LDS slice: one per lane (a 128-code block's part is one ordered sum, so
@@ -225,6 +226,7 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_kernel(BlockParams p) 
     float v = head * run;
     const size_t at = (size_t)m * N + r0 + rr;
     if (p.stages & TS_AFTER_ADD) v += p.a0[at];
+    if (p.after.count) v = after_apply(p.after, v, at);
     if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
     else ((float *)p.out)[at] = v;
 }
@@ -324,6 +326,7 @@ __global__ __launch_bounds__(kWaves * 64) void block_gemv_short_kernel(BlockPara
     float v = head * run;
     const size_t at = (size_t)m * N + r0 + rr;
     if (p.stages & TS_AFTER_ADD) v += p.a0[at];
+    if (p.after.count) v = after_apply(p.after, v, at);
     if (p.out_bf16) ((uint16_t *)p.out)[at] = bf16_bits(v);
     else ((float *)p.out)[at] = v;
 }
@@ -422,6 +425,8 @@ int block_gemv_launch(const ts_linear_args *a, void *stream) {
     BlockParams p;
     p.x = a->x; p.w = (const uint8_t *)a->w; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
+    const int rc = linear_after(a, "lanes (block form)", &p.after);
+    if (rc) return rc;
     {
         const BlockShape bs = block_shape(a->w_dtype);
         p.wide = (a->k / bs.block) * bs.bytes % 16 == 0 && aligned((const uint8_t *)a->w + bs.head, 16);

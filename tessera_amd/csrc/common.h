@@ -37,6 +37,11 @@ int hip_status(hipError_t e, const char *what);
 
 inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
+// A product's stage chain (ts_linear_args.after), checked (map.hip): an empty chain
+// when after is NULL; refused with TS_AFTER_ADD or TS_AFTER_ARGMAX, or with operands
+// that repeat.
+int linear_after(const ts_linear_args *a, const char *rule, ts_after *out);
+
 // The vector-ALU product for m <= 4 rows (gemv.hip); arguments already checked.
 int gemv_launch(const ts_linear_args *a, void *stream);
 
@@ -65,7 +70,9 @@ struct Route {
 size_t route_words(uint32_t rows, uint32_t count);
 int route_launch(const uint32_t *ids, uint32_t rows, uint32_t first, uint32_t count, uint32_t tile_rows, void *ws,
                  Route *route, void *stream);
-int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n, int out_bf16, void *stream);
+// Rows whose id is outside the set: their sum is 0, stored through the chain.
+int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n, int out_bf16, const ts_after &after,
+                       void *stream);
 
 }  // namespace ts
 

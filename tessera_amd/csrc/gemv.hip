@@ -23,7 +23,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
-#include "common.h"
+#include "after.h"
 
 namespace ts {
 
@@ -40,6 +40,7 @@ struct GemvParams {
     int out_bf16;
     void *keys;  // TS_AFTER_ARGMAX: [m] uint64
     uint32_t waves;  // waves per group splitting k
+    ts_after after;  // stage chain (count 0: none)
 };
 
 namespace {
@@ -274,6 +275,7 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
     }
     float v = silu ? g / (1.0f + expf(-g)) * u : g;
     if (p.stages & TS_AFTER_ADD) v += pre_a0;
+    if (p.after.count && live) v = after_apply(p.after, v, (size_t)m * N + n);
     if (live) {
         if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
         else ((float *)p.out)[(size_t)m * N + n] = v;
@@ -355,6 +357,8 @@ int gemv_launch(const ts_linear_args *a, void *stream) {
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.gain = a->gain; p.a0 = a->a0;
     p.out = a->out; p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.eps = a->eps;
     p.out_bf16 = a->out_dtype == TS_BF16; p.waves = w; p.keys = a->workspace;
+    const int rc = linear_after(a, "lanes (gemv)", &p.after);
+    if (rc) return rc;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
     Kern k = xf ? (w8 ? pick_m<true, true>(a->m, r) : pick_m<true, false>(a->m, r))
                 : (w8 ? pick_m<false, true>(a->m, r) : pick_m<false, false>(a->m, r));

@@ -19,7 +19,7 @@
 // bf16 parts (hi = bf16(x), lo = bf16(x - hi)), so f32 rows times bf16 weights stay
 // close to the f32 oracle. e4m3 weights decode to bf16 in registers; the per-row
 // scale multiplies the finished sum.
-#include "common.h"
+#include "after.h"
 
 #include <algorithm>
 
@@ -39,6 +39,7 @@ struct LanesParams {
     uint32_t stages;
     float eps;
     int out_bf16;
+    ts_after after;  // stage chain (count 0: none)
 };
 
 // Raw weight bytes of one lane (row `row`, lane group g) for the 128-deep chunk at
@@ -194,7 +195,7 @@ TS_DEV void store_x(const LanesParams &p, const float *inv, uint32_t k0, const X
 // per chunk (the 4 lanes of a row read contiguous runs, see load_w) into a register
 // ring D chunks deep, so D chunks of weights are in flight per wave. splits == 1: the epilogue runs here;
 // otherwise the raw sums go to part[s][SILU ? 2 : 1][m][n] for lanes_finish.
-template <int MT, bool XF32, bool W8, bool SILU, bool NORM>
+template <int MT, bool XF32, bool W8, bool SILU, bool NORM, bool CHAIN>
 __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float *part) {
     constexpr int D = (SILU && !W8) ? 2 : 4;     // weight chunks in flight per wave
     constexpr uint32_t kXBytes = 16 * MT * 256;  // one chunk of x rows, bf16
@@ -287,28 +288,45 @@ __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float
     // D lane layout: column col, rows 4 grp + r of each 16-row tile.
     const uint32_t n = n0 + col;
     if (n >= N) return;
+    if (splits > 1) {
+        float *dst = part + (size_t)split * (SILU ? 2 : 1) * M * N;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t m = 16 * t + 4 * grp + r;
+                if (m >= M) continue;
+                dst[(size_t)m * N + n] = acc_g[t][r];
+                if (SILU) dst[(size_t)M * N + (size_t)m * N + n] = acc_u[t][r];
+            }
+        return;
+    }
+    float val[MT * 4];
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t m = 16 * t + 4 * grp + r;
-            if (m >= M) continue;
             float g = acc_g[t][r], u = acc_u[t][r];
-            if (splits > 1) {
-                float *dst = part + (size_t)split * (SILU ? 2 : 1) * M * N;
-                dst[(size_t)m * N + n] = g;
-                if (SILU) dst[(size_t)M * N + (size_t)m * N + n] = u;
-                continue;
-            }
             if (W8) {
                 g *= bf16_float(p.w_scale[n]);
                 if (SILU) u *= bf16_float(p.w_scale[N + n]);
             }
-            float v = SILU ? silu(g) * u : g;
-            if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
-            if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
-            else ((float *)p.out)[(size_t)m * N + n] = v;
+            val[4 * t + r] = SILU ? silu(g) * u : g;
         }
+    // Value e: row 16 (e / 4) + 4 grp + e % 4.
+    auto row_of = [&](int e) { return 16 * (uint32_t)(e / 4) + 4 * grp + (uint32_t)(e % 4); };
+    if (CHAIN)  // the chain's variant: its values and sums need more registers
+        ts::after_values<MT * 4, false>(p.after, val, [&](int e) { return (size_t)row_of(e) * N + n; },
+                                        [&](int e) { return row_of(e) < M; });
+#pragma unroll
+    for (int e = 0; e < MT * 4; e++) {
+        const uint32_t m = row_of(e);
+        if (m >= M) continue;
+        float v = val[e];
+        if (p.stages & TS_AFTER_ADD) v += p.a0[(size_t)m * N + n];
+        if (p.out_bf16) ((uint16_t *)p.out)[(size_t)m * N + n] = bf16_bits(v);
+        else ((float *)p.out)[(size_t)m * N + n] = v;
+    }
 }
 
 // Sums the splits' partials in split order, then the epilogue.
@@ -343,6 +361,7 @@ __global__ __launch_bounds__(256) void lanes_finish(LanesParams p, const float *
     }
     float v = SILU ? silu(g) * u : g;
     if (p.stages & TS_AFTER_ADD) v += p.a0[i];
+    if (p.after.count) v = ts::after_apply(p.after, v, i);
     if (p.out_bf16) ((uint16_t *)p.out)[i] = bf16_bits(v);
     else ((float *)p.out)[i] = v;
 }
@@ -364,16 +383,21 @@ Plan plan(const ts_linear_args *a) {
 
 using Kern = void (*)(LanesParams, float *);
 
+template <int MT, bool XF32, bool W8, bool CHAIN>
+Kern pick4(bool silu, bool norm) {
+    if (silu) return norm ? lanes_kernel<MT, XF32, W8, true, true, CHAIN> : lanes_kernel<MT, XF32, W8, true, false, CHAIN>;
+    return norm ? lanes_kernel<MT, XF32, W8, false, true, CHAIN> : lanes_kernel<MT, XF32, W8, false, false, CHAIN>;
+}
+
 template <int MT, bool XF32, bool W8>
-Kern pick3(bool silu, bool norm) {
-    if (silu) return norm ? lanes_kernel<MT, XF32, W8, true, true> : lanes_kernel<MT, XF32, W8, true, false>;
-    return norm ? lanes_kernel<MT, XF32, W8, false, true> : lanes_kernel<MT, XF32, W8, false, false>;
+Kern pick3(bool silu, bool norm, bool chain) {
+    return chain ? pick4<MT, XF32, W8, true>(silu, norm) : pick4<MT, XF32, W8, false>(silu, norm);
 }
 
 template <int MT>
-Kern pick2(bool xf, bool w8, bool silu, bool norm) {
-    return xf ? (w8 ? pick3<MT, true, true>(silu, norm) : pick3<MT, true, false>(silu, norm))
-              : (w8 ? pick3<MT, false, true>(silu, norm) : pick3<MT, false, false>(silu, norm));
+Kern pick2(bool xf, bool w8, bool silu, bool norm, bool chain) {
+    return xf ? (w8 ? pick3<MT, true, true>(silu, norm, chain) : pick3<MT, true, false>(silu, norm, chain))
+              : (w8 ? pick3<MT, false, true>(silu, norm, chain) : pick3<MT, false, false>(silu, norm, chain));
 }
 
 int check(const ts_linear_args *a) {
@@ -415,7 +439,11 @@ extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
         return a->m <= 4 ? ts::block_gemv_launch(a, stream) : ts::block_tiled_launch(a, stream);
     int rc = check(a);
     if (rc) return rc;
-    if (a->m <= 4) return ts::gemv_launch(a, stream);
+    if (a->m <= 4) {
+        ts_after c;
+        rc = ts::linear_after(a, "lanes", &c);
+        return rc ? rc : ts::gemv_launch(a, stream);
+    }
     const Plan pl = plan(a);
     const size_t need = tessera_hip_lanes_workspace(a);
     if (need && (!a->workspace || a->workspace_bytes < need))
@@ -424,12 +452,15 @@ extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.gain = a->gain; p.a0 = a->a0;
     p.out = a->out; p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.eps = a->eps;
     p.out_bf16 = a->out_dtype == TS_BF16;
+    rc = ts::linear_after(a, "lanes", &p.after);
+    if (rc) return rc;
     const bool silu = a->stages & TS_AFTER_SILU_MUL, norm = a->stages & TS_BEFORE_RMS_NORM;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
     const uint32_t mt = (a->m + 15) / 16;
-    Kern k = mt == 1 ? pick2<1>(xf, w8, silu, norm)
-           : mt == 2 ? pick2<2>(xf, w8, silu, norm)
-           : mt == 3 ? pick2<3>(xf, w8, silu, norm) : pick2<4>(xf, w8, silu, norm);
+    const bool chain = p.after.count;
+    Kern k = mt == 1 ? pick2<1>(xf, w8, silu, norm, chain)
+           : mt == 2 ? pick2<2>(xf, w8, silu, norm, chain)
+           : mt == 3 ? pick2<3>(xf, w8, silu, norm, chain) : pick2<4>(xf, w8, silu, norm, chain);
     float *part = need ? (float *)a->workspace : nullptr;
     hipLaunchKernelGGL(k, dim3(pl.groups, pl.splits), dim3(kWaves * 64), 0, (hipStream_t)stream, p, part);
     TS_CHECK_LAUNCH("lanes launch");

@@ -14,7 +14,7 @@
 //   row_start[B + 1]  first sorted position of each bucket; row_start[B] = rows
 //   tile_start[count + 1]  first row tile of each matrix; tile_start[count] = total
 //   perm[rows]        perm[pos] = the row at sorted position pos
-#include "common.h"
+#include "after.h"
 
 namespace ts {
 
@@ -220,14 +220,15 @@ __global__ __launch_bounds__(kChunk) void route_place(const uint32_t *ids, uint3
 
 // Rows whose id is outside this rank's matrices read zeros (cpu.rs:100-102).
 __global__ __launch_bounds__(256) void zero_absent(const uint32_t *perm, const uint32_t *row_start, uint32_t count,
-                                                   void *out, uint32_t n, int out_bf16) {
+                                                   void *out, uint32_t n, int out_bf16, ts_after after) {
     const uint32_t from = row_start[count], to = row_start[count + 1];
     const uint64_t total = (uint64_t)(to - from) * n;
     for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256) {
         const uint32_t pos = from + (uint32_t)(i / n), col = (uint32_t)(i % n);
         const size_t at = (size_t)perm[pos] * n + col;
-        if (out_bf16) ((uint16_t *)out)[at] = 0;
-        else ((float *)out)[at] = 0.0f;
+        const float v = after.count ? after_apply(after, 0.0f, at) : 0.0f;
+        if (out_bf16) ((uint16_t *)out)[at] = bf16_bits(v);
+        else ((float *)out)[at] = v;
     }
 }
 
@@ -335,9 +336,10 @@ int route_launch(const uint32_t *ids, uint32_t rows, uint32_t first, uint32_t co
     return TS_OK;
 }
 
-int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n, int out_bf16, void *stream) {
+int zero_absent_launch(const Route &route, uint32_t count, void *out, uint32_t n, int out_bf16, const ts_after &after,
+                       void *stream) {
     hipLaunchKernelGGL(zero_absent, dim3(64), dim3(256), 0, (hipStream_t)stream, route.perm, route.row_start, count,
-                       out, n, out_bf16);
+                       out, n, out_bf16, after);
     TS_CHECK_LAUNCH("picked zero rows");
     return TS_OK;
 }

@@ -27,7 +27,7 @@
 //    three), e4m3 weights decode to bf16 on the way into LDS with the per-row
 //    scale applied to the finished sum; SiLU-gate pairs are laid out so a lane
 //    holds gate and up of the same column.
-#include "common.h"
+#include "after.h"
 
 namespace {
 
@@ -49,6 +49,7 @@ struct TiledParams {
     // matrix e's rows start at w + (e * stride + offset) * k (scales likewise).
     const uint32_t *perm, *row_start, *tile_start;
     uint32_t matrices, repeat, stride, offset;
+    ts_after after;  // stage chain (count 0: none)
 };
 
 // Byte offset of (row, chunk) in a swizzled [rows][8 chunks of 16B] tile.
@@ -135,7 +136,7 @@ struct Loader {
     }
 };
 
-template <int BT, bool XF32, bool W8, bool SILU, bool PICK>
+template <int BT, bool XF32, bool W8, bool SILU, bool PICK, bool CHAIN>
 __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
     constexpr int TILE = BT * BK * 2;         // bytes of one operand stage
     constexpr int WT = BT / 2, FT = WT / 16;  // wave tile, 16x16 fragments per wave side
@@ -227,16 +228,13 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
     const uint32_t N = p.n;
     const uint16_t *scale = ld.w_scale;
     const bool vec = (N & 3) == 0;
+    constexpr int JO = SILU ? FT / 2 : FT;
+    float val[FT][JO][4];
 #pragma unroll
-    for (int i = 0; i < FT; i++) {
-        const uint32_t tr = wm * WT + i * 16 + col;
-        if (m0 + tr >= mend) continue;
-        const uint32_t m = PICK ? rows_out[tr] : m0 + tr;
+    for (int i = 0; i < FT; i++)
 #pragma unroll
-        for (int j = 0; j < (SILU ? FT / 2 : FT); j++) {
+        for (int j = 0; j < JO; j++) {
             const uint32_t n = n0 + (SILU ? wn * (WT / 2) : wn * WT) + j * 16 + 4 * grp;
-            if (n >= N) continue;
-            float v[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 float g = acc[i][j][r];
@@ -246,12 +244,36 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
                         g *= bf16_float(scale[min(n + r, N - 1)]);
                         u *= bf16_float(scale[N + min(n + r, N - 1)]);
                     }
-                    v[r] = g / (1.0f + expf(-g)) * u;
+                    val[i][j][r] = g / (1.0f + expf(-g)) * u;
                 } else {
                     if (W8) g *= bf16_float(scale[min(n + r, N - 1)]);
-                    v[r] = g;
+                    val[i][j][r] = g;
                 }
             }
+        }
+    if (CHAIN) {  // the chain's variant: its values and sums need more registers
+        // Value e = (i JO + j) 4 + r: row tile i, column tile j, column 4 grp + r.
+        auto row_of = [&](int e) {
+            const uint32_t tr = wm * WT + (e / (4 * JO)) * 16 + col;
+            return m0 + tr < mend ? (PICK ? rows_out[tr] : m0 + tr) : ~0u;
+        };
+        auto col_of = [&](int e) {
+            return n0 + (SILU ? wn * (WT / 2) : wn * WT) + (e / 4 % JO) * 16 + 4 * grp + e % 4;
+        };
+        ts::after_values<FT * JO * 4, false>(
+            p.after, *(float(*)[FT * JO * 4])val, [&](int e) { return (size_t)row_of(e) * N + col_of(e); },
+            [&](int e) { return row_of(e) != ~0u && col_of(e) < N; });
+    }
+#pragma unroll
+    for (int i = 0; i < FT; i++) {
+        const uint32_t tr = wm * WT + i * 16 + col;
+        if (m0 + tr >= mend) continue;
+        const uint32_t m = PICK ? rows_out[tr] : m0 + tr;
+#pragma unroll
+        for (int j = 0; j < JO; j++) {
+            const uint32_t n = n0 + (SILU ? wn * (WT / 2) : wn * WT) + j * 16 + 4 * grp;
+            if (n >= N) continue;
+            float *v = val[i][j];
             const size_t at = (size_t)m * N + n;
             if (vec && n + 3 < N) {
                 if (p.stages & TS_AFTER_ADD) {
@@ -348,7 +370,7 @@ TS_DEV const char *uniform_ptr(const void *ptr) {
     return (const char *)(((uint64_t)hi << 32) | lo);
 }
 
-template <int TM, int TN, int KD, int NS, bool SILU, bool PICK>
+template <int TM, int TN, int KD, int NS, bool SILU, bool PICK, bool CHAIN>
 __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) {
     using P = Pipe<TM, TN, KD, NS>;
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -493,7 +515,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
     };
     constexpr int JO = SILU ? P::FJ / 2 : P::FJ;
     constexpr uint32_t WO = SILU ? P::WN / 2 : P::WN;
-    if (!PICK && p.out_bf16 && !(p.stages & TS_AFTER_ADD)) {
+    if (!PICK && p.out_bf16 && !(p.stages & TS_AFTER_ADD) && !p.after.count) {
         // bf16 rows through LDS: the tile as TM rows of OC bf16 (16-byte chunks
         // XOR-swizzled by row), then whole 16-byte chunks of rows to memory.
         constexpr uint32_t CH = OC / 8;  // chunks per output row
@@ -527,6 +549,24 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         return;
     }
     const bool vec = (N & 3) == 0;
+    float val[P::FI][JO][4];
+#pragma unroll
+    for (int i = 0; i < P::FI; i++)
+#pragma unroll
+        for (int j = 0; j < JO; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) val[i][j][r] = value(i, j, r);
+    if (CHAIN) {  // the chain's variant: its values and sums need more registers
+        // Value e = (i JO + j) 4 + r: row fragment i, column fragment j, column 4 grp + r.
+        auto row_of = [&](int e) {
+            const uint32_t tr = wm * P::WM + (e / (4 * JO)) * 16 + col;
+            return m0 + tr < mend ? (PICK ? rows_out[tr] : m0 + tr) : ~0u;
+        };
+        auto col_of = [&](int e) { return n0 + wn * WO + (e / 4 % JO) * 16 + 4 * grp + e % 4; };
+        ts::after_values<P::FI * JO * 4, false>(
+            p.after, *(float(*)[P::FI * JO * 4])val, [&](int e) { return (size_t)row_of(e) * N + col_of(e); },
+            [&](int e) { return row_of(e) != ~0u && col_of(e) < N; });
+    }
 #pragma unroll
     for (int i = 0; i < P::FI; i++) {
         const uint32_t tr = wm * P::WM + i * 16 + col;
@@ -536,9 +576,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         for (int j = 0; j < JO; j++) {
             const uint32_t n = n0 + wn * WO + j * 16 + 4 * grp;
             if (n >= N) continue;
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) v[r] = value(i, j, r);
+            float *v = val[i][j];
             const size_t at = (size_t)m * N + n;
             if (vec && n + 3 < N) {
                 if (p.stages & TS_AFTER_ADD) {
@@ -564,14 +602,19 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
 template <int TM, int TN, int KD, int NS, bool PICK>
 int pipe_launch(TiledParams p, bool silu, void *stream) {
     constexpr int lds = Pipe<TM, TN, KD, NS>::LDS;
-    static const hipError_t attr[2] = {
-        hipFuncSetAttribute((const void *)tiled_pipe_kernel<TM, TN, KD, NS, false, PICK>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds),
-        hipFuncSetAttribute((const void *)tiled_pipe_kernel<TM, TN, KD, NS, true, PICK>,
-                            hipFuncAttributeMaxDynamicSharedMemorySize, lds)};
-    if (attr[silu]) return ts::hip_status(attr[silu], "tiled (pipelined): LDS attribute");
-    const void *k = silu ? (const void *)tiled_pipe_kernel<TM, TN, KD, NS, true, PICK>
-                         : (const void *)tiled_pipe_kernel<TM, TN, KD, NS, false, PICK>;
+    const void *kerns[4] = {(const void *)tiled_pipe_kernel<TM, TN, KD, NS, false, PICK, false>,
+                            (const void *)tiled_pipe_kernel<TM, TN, KD, NS, true, PICK, false>,
+                            (const void *)tiled_pipe_kernel<TM, TN, KD, NS, false, PICK, true>,
+                            (const void *)tiled_pipe_kernel<TM, TN, KD, NS, true, PICK, true>};
+    // The dynamic LDS size is raised once per kernel (thread-safe static initialisation).
+    static const hipError_t attr[4] = {
+        hipFuncSetAttribute(kerns[0], hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+        hipFuncSetAttribute(kerns[1], hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+        hipFuncSetAttribute(kerns[2], hipFuncAttributeMaxDynamicSharedMemorySize, lds),
+        hipFuncSetAttribute(kerns[3], hipFuncAttributeMaxDynamicSharedMemorySize, lds)};
+    const int which = (silu ? 1 : 0) + (p.after.count ? 2 : 0);
+    if (attr[which]) return ts::hip_status(attr[which], "tiled (pipelined): LDS attribute");
+    const void *k = kerns[which];
     const uint32_t oc = silu ? TN / 2 : TN;
     const uint32_t gx = (p.n + oc - 1) / oc;
     dim3 grid;
@@ -602,14 +645,15 @@ bool pipe_fits(int x_dtype, int w_dtype, uint32_t x_rows, uint32_t k, uint32_t w
 using Kern = void (*)(TiledParams);
 
 template <int BT, bool XF32, bool W8, bool PICK>
-Kern pick_silu(bool silu) {
-    return silu ? tiled_kernel<BT, XF32, W8, true, PICK> : tiled_kernel<BT, XF32, W8, false, PICK>;
+Kern pick_silu(bool silu, bool chain) {
+    if (chain) return silu ? tiled_kernel<BT, XF32, W8, true, PICK, true> : tiled_kernel<BT, XF32, W8, false, PICK, true>;
+    return silu ? tiled_kernel<BT, XF32, W8, true, PICK, false> : tiled_kernel<BT, XF32, W8, false, PICK, false>;
 }
 
 template <int BT, bool PICK>
-Kern pick_kernel(bool xf, bool w8, bool silu) {
-    return xf ? (w8 ? pick_silu<BT, true, true, PICK>(silu) : pick_silu<BT, true, false, PICK>(silu))
-              : (w8 ? pick_silu<BT, false, true, PICK>(silu) : pick_silu<BT, false, false, PICK>(silu));
+Kern pick_kernel(bool xf, bool w8, bool silu, bool chain) {
+    return xf ? (w8 ? pick_silu<BT, true, true, PICK>(silu, chain) : pick_silu<BT, true, false, PICK>(silu, chain))
+              : (w8 ? pick_silu<BT, false, true, PICK>(silu, chain) : pick_silu<BT, false, false, PICK>(silu, chain));
 }
 
 }  // namespace
@@ -628,10 +672,12 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TS_REQUIRE((a->stages & ~(TS_AFTER_ADD | TS_AFTER_SILU_MUL)) == 0, "tiled: unknown stage bits %#x",
                a->stages);
     TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "tiled: x and w must be 16-byte aligned");
+    TiledParams p;
+    int rc = ts::linear_after(a, "tiled", &p.after);
+    if (rc) return rc;
     const int big = ts::tiled_big_launch(a, stream);
     if (big != 1) return big;
     const bool silu = a->stages & TS_AFTER_SILU_MUL;
-    TiledParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     // 64x64 tiles when 128x128 would give fewer than 2 groups per CU: more groups to
@@ -651,11 +697,13 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
         // tiles of 128 run 1.4-1.5x slower than with 512 of 64).
         const uint64_t oc = silu ? 64 : 128;
         const uint64_t tiles = (a->n + oc - 1) / oc * ((a->m + 127) / 128);
-        if (tiles >= 256) return pipe_launch<128, 128, 64, 2, false>(p, silu, stream);
+        // A stage chain takes 64 x 64 tiles: at 128 x 128 its values and sums spill.
+        if (tiles >= 256 && !p.after.count) return pipe_launch<128, 128, 64, 2, false>(p, silu, stream);
         return pipe_launch<64, 64, 64, 4, false>(p, silu, stream);
     }
-    Kern k = bt == 64 ? pick_kernel<64, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu)
-                      : pick_kernel<128, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
+    const bool chain = p.after.count;
+    Kern k = bt == 64 ? pick_kernel<64, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu, chain)
+                      : pick_kernel<128, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu, chain);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("tiled launch");
     return TS_OK;
@@ -678,7 +726,8 @@ static int picked_check(const ts_picked_args *a) {
     TS_REQUIRE(ts::aligned(a->x, 16) && ts::aligned(a->w, 16), "picked: x and w must be 16-byte aligned");
     TS_REQUIRE((uint64_t)a->rows / BM + a->count <= 65535, "picked: %u rows and %u matrices in one launch", a->rows,
                a->count);
-    return TS_OK;
+    ts_after c;
+    return ts::after_check(a->after, true, "picked", &c);
 }
 
 extern "C" size_t tessera_hip_picked_workspace(const ts_picked_args *a) {
@@ -698,9 +747,10 @@ extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
     int rc = ts::route_launch(a->ids, a->rows, a->first, a->count, BM, a->workspace, &route, stream);
     if (rc) return rc;
     const bool silu = a->stages & TS_AFTER_SILU_MUL;
-    rc = ts::zero_absent_launch(route, a->count, a->out, a->n, a->out_dtype == TS_BF16, stream);
-    if (rc) return rc;
     TiledParams p;
+    ts::after_check(a->after, true, "picked", &p.after);
+    rc = ts::zero_absent_launch(route, a->count, a->out, a->n, a->out_dtype == TS_BF16, p.after, stream);
+    if (rc) return rc;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = nullptr; p.out = a->out;
     p.m = a->rows; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     p.perm = route.perm; p.row_start = route.row_start; p.tile_start = route.tile_start;
@@ -708,8 +758,10 @@ extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
     const uint32_t cols = silu ? BN / 2 : BN;
     // Row tiles: at most one partial tile per matrix beyond rows / BM full ones.
     const uint32_t gx = (a->n + cols - 1) / cols, gy = (a->rows + BM - 1) / BM + a->count;
-    if (pipe_fits(a->x_dtype, a->w_dtype, a->rows, a->k, a->stride)) return pipe_launch<128, 128, 64, 2, true>(p, silu, stream);
-    Kern k = pick_kernel<BM, true>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu);
+    // A stage chain takes the register-staged kernel (the pipelined one's chain variant spills).
+    if (pipe_fits(a->x_dtype, a->w_dtype, a->rows, a->k, a->stride) && !p.after.count)
+        return pipe_launch<128, 128, 64, 2, true>(p, silu, stream);
+    Kern k = pick_kernel<BM, true>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu, p.after.count != 0);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("picked launch");
     return TS_OK;

@@ -223,6 +223,9 @@ __global__ __launch_bounds__(kThreads, 1) void tiled_big_kernel(BigParams p) {
 // least ~one tile per CU); returns 1 when it did not apply.
 int tiled_big_launch(const ts_linear_args *a, void *stream) {
     if (a->x_dtype != TS_BF16 || a->w_dtype != TS_BF16 || (a->stages & TS_AFTER_SILU_MUL)) return 1;
+    // A stage chain takes the 128x128 kernel: its values per lane (128 here) would need
+    // a second 128 registers for the chain's sums.
+    if (a->after) return 1;
     if (a->k % BK != 0) return 1;  // whole 64-deep steps: loads go straight to LDS, no zero fill
     const uint32_t gx = (a->n + BN - 1) / BN, gy = (a->m + BM - 1) / BM;
     if ((uint64_t)gx * gy < 240 || gy > 65535) return 1;

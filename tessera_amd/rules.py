@@ -59,6 +59,35 @@ BLOCK_FORMS = {"q8_0": abi.TS_Q8_0, "mxfp8": abi.TS_MXFP8, "int4_g32": abi.TS_IN
                "nvfp4": abi.TS_NVFP4, "mxfp4": abi.TS_MXFP4, "int4_g128": abi.TS_INT4_G128}
 
 
+def chain(stages, operands=(), *, sum_at=0, spans=None):
+    """A stage chain (ts_after) for a product's epilogue or for map(): `stages` in order,
+    each "add", "mul", ("scale", by) or an activation name ("gelu_tanh", "silu",
+    "sigmoid", "relu", "softplus", "exp", "tanh"); `operands` the f32 tensors the Add /
+    Mul stages read, in order; `sum_at` which of the chain's reads is the sum (or map's
+    input). engine/plan/lower/src/kernels/map.rs:40-59,125-185. The tensors must stay
+    alive until the call has been enqueued (the struct holds their addresses)."""
+    c = abi.After()
+    if len(stages) > abi.TS_MAP_STAGES or len(operands) > abi.TS_MAP_OPERANDS:
+        raise ValueError(f"at most {abi.TS_MAP_STAGES} stages and {abi.TS_MAP_OPERANDS} operands")
+    for i, st in enumerate(stages):
+        if st == "add":
+            c.stage[i].op = abi.TS_MAP_ADD
+        elif st == "mul":
+            c.stage[i].op = abi.TS_MAP_MUL
+        elif isinstance(st, tuple) and st[0] == "scale":
+            c.stage[i].op, c.stage[i].by = abi.TS_MAP_SCALE, float(st[1])
+        else:
+            c.stage[i].op, c.stage[i].act = abi.TS_MAP_ACT, abi.ACTS[st]
+    for j, t in enumerate(operands):
+        if t.dtype != torch.float32:
+            raise ValueError("chain operands are f32")
+        c.operand[j] = t.data_ptr()
+        c.spans[j] = (spans or [0] * len(operands))[j]
+    c.count, c.sum = len(stages), sum_at
+    c._keep = list(operands)
+    return c
+
+
 def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e-6, w_form=None):
     m, k = x.shape
     n = out.shape[1]
@@ -74,8 +103,9 @@ def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e
 
 
 def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, gain=None, a0=None,
-            silu_mul=False, eps=1e-6, w_form=None, rows=None):
-    """rows: the weight rows of a packed block-form tensor (w is then flat bytes)."""
+            silu_mul=False, eps=1e-6, w_form=None, rows=None, after=None):
+    """rows: the weight rows of a packed block-form tensor (w is then flat bytes).
+    after: a chain() run on each sum before the store."""
     m = x.shape[0]
     wr = rows if w_form is not None else w.shape[0]
     if wr is None:
@@ -86,6 +116,8 @@ def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, g
     stages = (abi.TS_AFTER_ADD if a0 is not None else 0) | (abi.TS_AFTER_SILU_MUL if silu_mul else 0) | \
         (abi.TS_BEFORE_RMS_NORM if gain is not None else 0)
     a = linear_args(x, w, out, w_scale=w_scale, gain=gain, a0=a0, stages=stages, eps=eps, w_form=w_form)
+    if after is not None:
+        a.after = C.addressof(after)
     lib = abi.load()
     need = getattr(lib, fn + "_workspace")(C.byref(a)) if hasattr(lib, fn + "_workspace") else 0
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)
@@ -109,7 +141,7 @@ def tiled(x, w, **kw):
 
 
 def picked(x, w, ids, *, n=None, repeat=1, first=0, offset=0, silu_mul=False, w_scale=None, out=None,
-           out_dtype=torch.float32):
+           out_dtype=torch.float32, after=None):
     """Rule "picked": row r multiplies matrix ids[r] - first of the set w [count, stride, k]
     (rows offset..offset+n, or the gate/up pair with silu_mul); x row r // repeat."""
     count, stride, k = w.shape
@@ -123,9 +155,22 @@ def picked(x, w, ids, *, n=None, repeat=1, first=0, offset=0, silu_mul=False, w_
     a.rows, a.n, a.k, a.count, a.stride, a.offset, a.repeat, a.first = rows, n, k, count, stride, offset, repeat, first
     a.x_dtype, a.w_dtype, a.out_dtype = _DT[x.dtype], _DT[w.dtype], _DT[out.dtype]
     a.stages = abi.TS_AFTER_SILU_MUL if silu_mul else 0
+    if after is not None:
+        a.after = C.addressof(after)
     need = abi.load().tessera_hip_picked_workspace(C.byref(a))
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)
     abi.call("tessera_hip_picked", C.byref(a), _stream())
+    return out
+
+
+def map(x, stages, operands=(), *, sum_at=0, spans=None, out=None):
+    """Rule "map": out = chain(x) elementwise over f32 x (map.rs:60-65,187-260)."""
+    if out is None:
+        out = torch.empty_like(x)
+    a = abi.MapArgs()
+    a.x, a.out, a.len = _ptr(x), _ptr(out), x.numel()
+    a.after = chain(stages, operands, sum_at=sum_at, spans=spans)
+    abi.call("tessera_hip_map", C.byref(a), _stream())
     return out
 
 

@@ -17,7 +17,7 @@ def test_exports_every_declared_function():
     arity = abi.declared_arity()
     for name, (_, args) in sigs.items():
         assert arity[name] == len(args), (name, arity[name], len(args))
-    assert lib.tessera_hip_abi_version() == 3
+    assert lib.tessera_hip_abi_version() == 4
 
 
 def test_argument_errors_need_no_device():
@@ -41,12 +41,13 @@ def test_argument_errors_need_no_device():
 
 def test_struct_layout_matches_header():
     # Offsets the C compiler gives the header's structs (x86-64 SysV).
-    assert C.sizeof(abi.LinearArgs) == 8 * 8 + 4 * 8
-    assert abi.LinearArgs.m.offset == 64 and abi.LinearArgs.eps.offset == 92
+    assert C.sizeof(abi.LinearArgs) == 8 * 8 + 4 * 8 + 8
+    assert abi.LinearArgs.m.offset == 64 and abi.LinearArgs.eps.offset == 92 and abi.LinearArgs.after.offset == 96
     assert abi.RowsArgs.rows.offset == 72 and abi.RowsArgs.max_position.offset == 120
     assert abi.RowsArgs.status.offset == 128 and C.sizeof(abi.RowsArgs) == 136
-    assert C.sizeof(abi.PickedArgs) == 104
+    assert C.sizeof(abi.PickedArgs) == 112
     assert abi.PickedArgs.rows.offset == 56 and abi.PickedArgs.stages.offset == 100
+    assert C.sizeof(abi.After) == 32 + 16 + 8 + 8 * 12
 
 
 STRUCTS = {
@@ -55,7 +56,10 @@ STRUCTS = {
     "ts_qk_args": "QkArgs", "ts_gather_args": "GatherArgs", "ts_take_args": "TakeArgs",
     "ts_softmax_args": "SoftmaxArgs", "ts_mix_args": "MixArgs", "ts_argmax_args": "ArgmaxArgs",
     "ts_keys_args": "KeysArgs", "ts_top_k_args": "TopKArgs", "ts_step_args": "StepArgs",
+    "ts_map_stage": "MapStage", "ts_after": "After", "ts_map_args": "MapArgs",
 }
+# include/tessera_kv.h's structs and their bindings in tessera_amd/kv.py.
+KV_STRUCTS = {"ts_kv_run": "RunId", "ts_kv_copy": "PageCopy", "ts_kv_stats": "Stats", "ts_kv_copy_args": "CopyArgs"}
 
 
 def test_every_struct_matches_the_compiler(tmp_path):
@@ -66,14 +70,18 @@ def test_every_struct_matches_the_compiler(tmp_path):
     import pytest
     if shutil.which("gcc") is None:
         pytest.skip("no gcc")
-    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{abi.HEADER}"', "int main(void) {"]
+    import os
+    from tessera_amd import kv
+    kv_header = os.path.join(os.path.dirname(abi.HEADER), "tessera_kv.h")
+    lines = ['#include <stddef.h>', '#include <stdio.h>', f'#include "{abi.HEADER}"', f'#include "{kv_header}"',
+             "int main(void) {"]
     want = []
-    for cname, pname in STRUCTS.items():
-        st = getattr(abi, pname)
+    pairs = [(c, getattr(abi, p)) for c, p in STRUCTS.items()] + [(c, getattr(kv, p)) for c, p in KV_STRUCTS.items()]
+    for cname, st in pairs:
         lines.append(f'printf("%zu\\n", sizeof({cname}));')
         want.append(C.sizeof(st))
         for field, _ in st._fields_:
-            lines.append(f'printf("%zu\\n", offsetof({cname}, {field}));')
+            lines.append(f'printf("%zu\\n", offsetof({cname}, {field.rstrip("_")}));')  # from_: C's `from`
             want.append(getattr(st, field).offset)
     lines.append("return 0; }")
     src = tmp_path / "layout.c"
@@ -170,3 +178,41 @@ def test_flash_rows_refuses_more_row_groups_than_its_order_packs():
     r.rows = 65535 * 128 + 1
     assert lib.tessera_hip_flash_rows(C.byref(r), None) == abi.TS_ERR_ARG
     assert b"rows in one launch" in lib.tessera_hip_last_error()
+
+
+def test_stage_chain_refusals_need_no_device():
+    """Stage chains the library refuses before anything launches (fake addresses are
+    never dereferenced on these paths): too many stages, an unknown activation, an
+    operand missing, a repeating operand on a product, a chain with TS_AFTER_ADD."""
+    import pytest
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("fake device addresses are only passed where no GPU could run them")
+    lib = abi.load()
+    fake = 1 << 20
+    m = abi.MapArgs()
+    m.x = m.out = fake
+    m.len = 16
+    m.after.count = 9
+    assert lib.tessera_hip_map(C.byref(m), None) == abi.TS_ERR_ARG and b"stages" in lib.tessera_hip_last_error()
+    m.after.count = 1
+    m.after.stage[0].op, m.after.stage[0].act = abi.TS_MAP_ACT, 7
+    assert lib.tessera_hip_map(C.byref(m), None) == abi.TS_ERR_ARG and b"activation" in lib.tessera_hip_last_error()
+    m.after.stage[0].op = abi.TS_MAP_ADD
+    assert lib.tessera_hip_map(C.byref(m), None) == abi.TS_ERR_ARG and b"NULL" in lib.tessera_hip_last_error()
+    m.after.sum = 2
+    m.after.operand[0] = fake
+    assert lib.tessera_hip_map(C.byref(m), None) == abi.TS_ERR_ARG and b"sum" in lib.tessera_hip_last_error()
+    after = abi.After()
+    after.count, after.operand[0], after.spans[0] = 1, fake, 4
+    after.stage[0].op = abi.TS_MAP_MUL
+    a = abi.LinearArgs()
+    a.x = a.w = a.out = fake
+    a.m, a.n, a.k = 1, 8, 64
+    a.x_dtype, a.w_dtype, a.out_dtype = abi.TS_F32, abi.TS_BF16, abi.TS_F32
+    a.after = C.addressof(after)
+    assert lib.tessera_hip_lanes(C.byref(a), None) == abi.TS_ERR_ARG and b"repeats" in lib.tessera_hip_last_error()
+    after.spans[0] = 0
+    a.stages, a.a0 = abi.TS_AFTER_ADD, fake
+    assert lib.tessera_hip_linear(C.byref(a), None) == abi.TS_ERR_ARG
+    assert b"TS_AFTER_ADD" in lib.tessera_hip_last_error()

@@ -336,3 +336,46 @@ def test_threads_bit_identical():
     b = O.product_bf16w(x, w)
     O.set_threads(1)
     assert np.array_equal(a, b)
+
+
+def test_act_against_closed_forms():
+    """Every activation of the oracle (cpu.rs:8-29) against its formula in float64 on a
+    dense grid: within 4e-7 relative (the f32 rounding of each step) plus 1e-37."""
+    x = np.concatenate([np.linspace(-20, 20, 8001), [0.0, 1e-6, -1e-6, 50.0, -50.0]]).astype(np.float32)
+    d = x.astype(np.float64)
+    forms = {
+        "gelu_tanh": 0.5 * d * (1 + np.tanh(0.7978846 * (d + 0.044715 * d ** 3))),
+        "silu": d / (1 + np.exp(-d)),
+        "sigmoid": 1 / (1 + np.exp(-d)),
+        "relu": np.maximum(d, 0),
+        "softplus": np.maximum(d, 0) + np.log1p(np.exp(-np.abs(d))),
+        "exp": np.exp(d),
+        "tanh": np.tanh(d),
+    }
+    for a, want in forms.items():
+        got = O.act(a, x).astype(np.float64)
+        # gelu's inner sum cancels near x = 0 only where the result is tiny
+        tol = 1e-6 * np.abs(want) + 1e-37 + (1e-7 if a == "gelu_tanh" else 0)
+        assert np.all(np.abs(got - want) <= tol), a
+
+
+def test_chain_known_answers():
+    """The chain's read order (kernels/map.rs:125-185): read `sum_at` is the input, the
+    others the operands in order; each stage one f32 rounding (cpu.rs:353-390)."""
+    x = np.array([1.0, 2.0], np.float32)
+    a = np.array([3.0, 4.0], np.float32)
+    b = np.array([0.5, -1.0], np.float32)
+    # v = x; v = v + a; v = v * b; v = v * 2
+    close(O.chain(x, ["add", "mul", ("scale", 2.0)], [a, b], 0), [4.0, -12.0])
+    # the input read second: v = a; v = v + x; v = v * b
+    close(O.chain(x, ["add", "mul"], [a, b], 1), [2.0, -6.0])
+    # the input read last: v = a; v = v * b; v = v + x
+    close(O.chain(x, ["mul", "add"], [a, b], 2), [2.5, -2.0])
+    # spans: a row of 2 repeating, and a scalar
+    r = np.array([10.0, 20.0], np.float32)
+    close(O.chain(np.arange(4, dtype=np.float32), ["add", "mul"], [r, np.array([3.0], np.float32)], 0, [2, 1]),
+          [30.0, 63.0, 36.0, 69.0])
+    # each stage rounds: (1 + 2^-24) + 2^-24 = 1 twice over in f32, not 1 + 2^-23
+    tiny = np.float32(2.0 ** -24)
+    assert O.chain(np.array([1.0], np.float32), ["add", "add"], [np.array([tiny]), np.array([tiny])])[0] == 1.0
+    close(O.chain(np.array([-2.0, 3.0], np.float32), ["relu", "exp"]), [1.0, float(np.exp(np.float32(3.0)))])
