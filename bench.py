@@ -357,6 +357,23 @@ def c5(torch):
             "frac": round(roof / t, 4)}
 
 
+def host_cpu():
+    """The host the CPU baseline ran on: its logical cores, the ones this process may
+    use, and the CPU model. The baseline uses at most 16 threads, the CPU share of one
+    GPU on these boxes."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"host_cores": os.cpu_count(), "host_cores_usable": len(os.sched_getaffinity(0)), "cpu_model": model,
+            "thread_cap": 16}
+
+
 def cpu_baseline(model, prompt, steps, threads=None):
     """The oracle decoding `steps` tokens after the same prompt, kept rows copied from
     the device after its prefill; `threads` host cores (default: all, up to 16) via
@@ -385,7 +402,7 @@ def cpu_baseline(model, prompt, steps, threads=None):
         tok = int(np.argmax(logits))
     dt = time.perf_counter() - t0
     how = f"OpenMP over output columns, {threads} threads" if threads > 1 else "one thread, reference order"
-    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port", **host_cpu(),
             "sample": f"{steps} greedy decode steps at context {PROMPT}..{PROMPT + steps} "
                       f"(oracle restatement of tessera-interp, {how})"}
 

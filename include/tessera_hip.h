@@ -291,6 +291,36 @@ typedef struct {
 int tessera_hip_map(const ts_map_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------
+ * Whole-sequence attention with any mask (the reference's flash on the Attend site,
+ * engine/rules/attention/src/flash.rs:416-503; semantics of interp's attend,
+ * engine/ir/interp/src/cpu.rs:61-77,172-225, masks engine/ir/graph/src/node.rs:162-
+ * 181). Query i of a sequence sits at position past + i, past = keys - rows when the
+ * keys cover the rows (ends aligned), else 0 (refused for causal masks); it sees keys
+ * [pos - back, pos + ahead] of its sequence, p = softmax(dot(q, k) * scale); a query
+ * whose window holds no key writes zeros. Masks: Causal (back UINT32_MAX, ahead 0,
+ * causal 1), Bidirectional (UINT32_MAX, UINT32_MAX, 0), Within(n) (n, n, 0), Back(n)
+ * (n, 0, 1). Head h reads kv head h / (heads / kv_heads).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const void *q;      /* [seqs, rows, heads, width] f32 or bf16 */
+    const void *k;      /* [seqs, keys, kv_heads, width] bf16 */
+    const void *v;      /* [seqs, keys, kv_heads, width] bf16 */
+    void *out;          /* [seqs, rows, heads, width] f32 */
+    uint32_t seqs, rows, keys, heads, kv_heads;
+    uint32_t width;     /* 128 */
+    uint32_t back, ahead;
+    int32_t causal;     /* the mask is causal (Causal, Back): more rows than keys is refused */
+    float scale;
+    int32_t q_dtype, kv_dtype, out_dtype;
+} ts_flash_args;
+
+/* Same kernel as tessera_hip_flash_rows: 128-row query blocks on the matrix unit, keys
+ * streamed in 64-key blocks with online softmax.
+ * Replaces: rule "flash" on whole sequences (engine/rules/attention/src/flash.rs:
+ * 416-503, 775-807). */
+int tessera_hip_flash(const ts_flash_args *a, void *stream);
+
+/* ----------------------------------------------------------------------------
  * Row stages and indices. Each takes one argument struct, fields in the reference
  * Launch order (reads, outputs, then counts and scalars), and the stream.
  * ------------------------------------------------------------------------- */

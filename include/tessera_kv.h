@@ -92,7 +92,8 @@ uint64_t tessera_kv_error_value2(const ts_kv_pool *p);
  * ------------------------------------------------------------------------- */
 
 /* Status bit (ORed into ts_kv_copy_args.status): a copy named a page >= pages, more
- * rows than a page, a page onto itself, or a buffer not 16-byte aligned; it was
+ * rows than a page, a page onto itself, a buffer not 16-byte aligned, or a target page
+ * that another copy of the same call reads or writes (copies run at once); it was
  * skipped. */
 #define TS_KV_STATUS_COPY 2u
 

@@ -126,6 +126,10 @@ KeysArgs = _args("KeysArgs", "ts_keys_args", [
     ("keys", _v), ("ids", _v), ("rows", _u), ("width", _u)])
 TopKArgs = _args("TopKArgs", "ts_top_k_args", [
     ("x", _v), ("ids", _v), ("rows", _u), ("width", _u), ("k", _u)])
+FlashArgs = _args("FlashArgs", "ts_flash_args", [
+    ("q", _v), ("k", _v), ("v", _v), ("out", _v), ("seqs", _u), ("rows", _u), ("keys", _u), ("heads", _u),
+    ("kv_heads", _u), ("width", _u), ("back", _u), ("ahead", _u), ("causal", C.c_int32), ("scale", _f),
+    ("q_dtype", C.c_int32), ("kv_dtype", C.c_int32), ("out_dtype", C.c_int32)])
 StepArgs = _args("StepArgs", "ts_step_args", [
     ("rows", RowsArgs), ("qkv", _v), ("q_gain", _v), ("k_gain", _v), ("rope_table", _v),
     ("rope_rows", _u), ("eps", _f)])
@@ -167,6 +171,7 @@ SIGNATURES = {
     "tessera_hip_argmax_keys": (C.c_int, [C.POINTER(KeysArgs), _P]),
     "tessera_hip_top_k": (C.c_int, [C.POINTER(TopKArgs), _P]),
     "tessera_hip_map": (C.c_int, [C.POINTER(MapArgs), _P]),
+    "tessera_hip_flash": (C.c_int, [C.POINTER(FlashArgs), _P]),
 }
 
 

@@ -1015,13 +1015,11 @@ int decode_step_groups(uint32_t *groups) {
 }
 
 int decode_step_launch(const DecodeStepArgs *a, void *stream) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_step_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
-        if (e != hipSuccess) return hip_status(e, "decode_step: shared memory attribute");
-        attr = true;
-    }
+    // Raised once per process; C++ makes the static's initialisation thread-safe, and
+    // every call returns the stored outcome.
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void *)decode_step_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (attr != hipSuccess) return hip_status(attr, "decode_step: shared memory attribute");
     DecodeStepArgs args = *a;
     if (!plan_roles(a->H, a->Hq, a->Hkv, a->F, a->NG, args.role_first, args.role_count))
         return fail(TS_ERR_ARG, "decode_step: %u groups cannot hold this shape", a->NG);

@@ -47,7 +47,21 @@ struct FlashParams {
     uint32_t rows, keys, heads, kv_heads, back, kept_pages, page_shift, max_position;
     float scale;
     uint32_t *status;
+    // Whole sequences (seq_rows > 0, slots and positions NULL): row r is query r %
+    // seq_rows of sequence r / seq_rows, at position past + r % seq_rows, and sees keys
+    // [pos - back, pos + ahead] of its sequence (engine/ir/interp/src/cpu.rs:61-77
+    // seen); a row whose window holds no key writes zeros. Ragged rows: ahead = 0.
+    uint32_t ahead, seq_rows, past;
 };
+
+// The slot and position of row r, and the last key its window reaches.
+TS_DEV uint32_t row_slot(const FlashParams &p, uint32_t r) { return p.seq_rows ? r / p.seq_rows : p.slots[r]; }
+TS_DEV uint32_t row_pos(const FlashParams &p, uint32_t r) {
+    return p.seq_rows ? p.past + r % p.seq_rows : p.positions[r];
+}
+TS_DEV uint32_t row_to(const FlashParams &p, uint32_t pos) {
+    return p.seq_rows ? (uint32_t)min((uint64_t)pos + p.ahead, (uint64_t)p.keys - 1) : pos;
+}
 
 TS_DEV uint64_t kept_row(const FlashParams &p, uint32_t slot, uint32_t pos) {
     if (!p.table) return (uint64_t)slot * p.keys + pos;
@@ -127,8 +141,9 @@ TS_DEV uint32_t widest_first(const FlashParams &p, uint32_t lane, uint32_t wave,
             his[u] = 0;
             los[u] = 0xffffffffu;
             if (half < 2 * ng && r < p.rows) {
-                his[u] = min(p.positions[r], p.max_position);
-                los[u] = his[u] > p.back ? his[u] - p.back : 0;
+                const uint32_t pos = min(row_pos(p, r), p.max_position);
+                his[u] = row_to(p, pos);
+                los[u] = pos > p.back ? pos - p.back : 0;
             }
         }
 #pragma unroll
@@ -203,10 +218,14 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         srange[t][1] = 0;
         spass[t] = kNoPass;
         if (r0 + t < p.rows) {
-            const uint32_t pos = p.positions[r0 + t];
-            ok_t = !(pos >= p.keys || pos > p.max_position || (p.table && (pos >> p.page_shift) >= p.kept_pages));
-            if (!ok_t && p.status) atomicOr(p.status, TS_STATUS_POSITION);
-            slot_t = p.slots[r0 + t];
+            const uint32_t pos = row_pos(p, r0 + t);
+            if (p.seq_rows) {  // whole sequences: served when the window holds a key
+                ok_t = pos < p.keys + (uint64_t)p.back && (pos > p.back ? pos - p.back : 0) <= row_to(p, pos);
+            } else {
+                ok_t = !(pos >= p.keys || pos > p.max_position || (p.table && (pos >> p.page_shift) >= p.kept_pages));
+                if (!ok_t && p.status) atomicOr(p.status, TS_STATUS_POSITION);
+            }
+            slot_t = row_slot(p, r0 + t);
         }
     }
     if (t == 0) { smixed = 0; snpass = 0; }
@@ -250,9 +269,9 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     __syncthreads();
     if (!smixed && t == 0) sslot[0] = lead0;
     if (t < kRows && ok_t) {
-        const uint32_t pos = p.positions[r0 + t];
+        const uint32_t pos = row_pos(p, r0 + t);
         atomicMin(&srange[spass[t]][0], pos > p.back ? pos - p.back : 0);
-        atomicMax(&srange[spass[t]][1], pos);
+        atomicMax(&srange[spass[t]][1], row_to(p, pos));
     }
     __syncthreads();
     const uint32_t npass = snpass;
@@ -275,8 +294,9 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         const uint32_t i = 16 * kQT * qw + 16 * qt + col, r = r0 + i;
         rpass[qt] = spass[i];
         rlive[qt] = rpass[qt] != kNoPass;
-        rpos[qt] = rlive[qt] ? p.positions[r] : 0;
-        rfrom[qt] = rpos[qt] > p.back ? rpos[qt] - p.back : 0;
+        const uint32_t pos = rlive[qt] ? row_pos(p, r) : 0;
+        rpos[qt] = row_to(p, pos);  // the last key the row sees
+        rfrom[qt] = pos > p.back ? pos - p.back : 0;
         if (!QF32) {
             const uint16_t *qr = (const uint16_t *)p.q + ((size_t)(rlive[qt] ? r : 0) * p.heads + h) * 128 + 32 * grp;
 #pragma unroll
@@ -486,16 +506,40 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     }  // pass
 
     // O / l: lane (query col of tile qt) holds d = 16 dt + 4 grp + i. Refused rows
-    // write NaN.
+    // write NaN; whole-sequence rows that see no key write zeros.
 #pragma unroll
     for (int qt = 0; qt < kQT; qt++) {
         const uint32_t r = r0 + 16 * kQT * qw + 16 * qt + col;
         if (r >= p.rows) continue;
         float *dst = p.out + ((size_t)r * p.heads + h) * 128;
-        const float inv = rlive[qt] ? 1.0f / l[qt] : __builtin_nanf("");
+        const float inv = rlive[qt] ? 1.0f / l[qt] : p.seq_rows ? 0.0f : __builtin_nanf("");
 #pragma unroll
         for (int d = 0; d < 8; d++) *(f32x4 *)(dst + d * 16 + 4 * grp) = o[qt][d] * inv;
     }
+}
+
+int flash_launch(const FlashParams &p, bool f32, void *stream, const char *rule) {
+    // Two q heads per group when the kv heads are shared in pairs (or more, evenly).
+    const int hg = (p.heads / p.kv_heads) % 2 == 0 ? 2 : 1;
+    const auto kern = hg == 2 ? (f32 ? flash_rows_kernel<true, 2> : flash_rows_kernel<false, 2>)
+                              : (f32 ? flash_rows_kernel<true, 1> : flash_rows_kernel<false, 1>);
+    // The key blocks' dynamic LDS, raised once per process (thread-safe static
+    // initialisation; every call returns the stored outcome).
+    static const hipError_t attr = [] {
+        for (const auto k : {flash_rows_kernel<true, 2>, flash_rows_kernel<false, 2>, flash_rows_kernel<true, 1>,
+                             flash_rows_kernel<false, 1>}) {
+            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     2 * kBlockBytes);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }();
+    if (attr != hipSuccess) return ts::hip_status(attr, "flash: shared memory attribute");
+    hipLaunchKernelGGL(kern, dim3((p.rows + kRows - 1) / kRows, p.heads / hg), dim3(256 * hg), 2 * kBlockBytes,
+                       (hipStream_t)stream, p);
+    const hipError_t e = hipPeekAtLastError();
+    if (e != hipSuccess) return ts::hip_status(e, rule);
+    return TS_OK;
 }
 
 }  // namespace
@@ -522,23 +566,37 @@ extern "C" int tessera_hip_flash_rows(const ts_rows_args *a, void *stream) {
     p.rows = a->rows; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads; p.back = a->back;
     p.kept_pages = a->kept_pages; p.page_shift = a->kept_table ? (uint32_t)__builtin_ctz(a->page) : 0;
     p.scale = a->scale; p.max_position = a->max_position; p.status = a->status;
-    // Two q heads per group when the kv heads are shared in pairs (or more, evenly).
-    const int hg = (a->heads / a->kv_heads) % 2 == 0 ? 2 : 1;
-    const bool f32 = a->q_dtype == TS_F32;
-    const auto kern = hg == 2 ? (f32 ? flash_rows_kernel<true, 2> : flash_rows_kernel<false, 2>)
-                              : (f32 ? flash_rows_kernel<true, 1> : flash_rows_kernel<false, 1>);
-    static bool attr = false;
-    if (!attr) {  // the key blocks (dynamic) plus the static tables
-        for (const auto k : {flash_rows_kernel<true, 2>, flash_rows_kernel<false, 2>, flash_rows_kernel<true, 1>,
-                             flash_rows_kernel<false, 1>}) {
-            const hipError_t e = hipFuncSetAttribute((const void *)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                     2 * kBlockBytes);
-            if (e != hipSuccess) return ts::hip_status(e, "flash_rows: shared memory attribute");
-        }
-        attr = true;
-    }
-    hipLaunchKernelGGL(kern, dim3((a->rows + kRows - 1) / kRows, a->heads / hg), dim3(256 * hg), 2 * kBlockBytes,
-                       (hipStream_t)stream, p);
-    TS_CHECK_LAUNCH("flash_rows launch");
-    return TS_OK;
+    p.ahead = 0; p.seq_rows = 0; p.past = 0;
+    return flash_launch(p, a->q_dtype == TS_F32, stream, "flash_rows");
+}
+
+extern "C" int tessera_hip_flash(const ts_flash_args *a, void *stream) {
+    TS_REQUIRE(a && a->q && a->k && a->v && a->out, "flash: null pointer");
+    TS_REQUIRE(a->width == 128, "flash: head width %u (128 supported)", a->width);
+    TS_REQUIRE(a->kv_heads >= 1 && a->heads % a->kv_heads == 0, "flash: %u heads over %u kv heads", a->heads,
+               a->kv_heads);
+    TS_REQUIRE((a->q_dtype == TS_F32 || a->q_dtype == TS_BF16) && a->kv_dtype == TS_BF16 && a->out_dtype == TS_F32,
+               "flash: q f32 or bf16, k and v bf16, out f32 supported");
+    TS_REQUIRE(a->keys >= 1 && a->rows >= 1, "flash: rows %u, keys %u", a->rows, a->keys);
+    // interp's attend (cpu.rs:61-77): query and key ends align when the keys cover the
+    // rows; fewer keys than rows are refused for masks whose ends align (causal, back).
+    TS_REQUIRE(a->keys >= a->rows || !a->causal, "flash: %u rows over %u keys with a causal mask", a->rows, a->keys);
+    TS_REQUIRE(ts::aligned(a->k, 16) && ts::aligned(a->v, 16) && ts::aligned(a->q, 16),
+               "flash: q, k, v must be 16-byte aligned");
+    TS_REQUIRE(a->heads <= 65535, "flash: grid limits");
+    const uint64_t total = (uint64_t)a->seqs * a->rows;
+    TS_REQUIRE(total <= 65535u * 128u, "flash: %llu rows in one launch (at most %u)", (unsigned long long)total,
+               65535u * 128u);
+    TS_REQUIRE((uint64_t)a->seqs * a->keys < (1ull << 32), "flash: %u sequences of %u keys", a->seqs, a->keys);
+    if (total == 0) return TS_OK;
+    FlashParams p;
+    p.q = a->q; p.k = (const uint16_t *)a->k; p.v = (const uint16_t *)a->v; p.out = (float *)a->out;
+    p.slots = p.positions = p.table = nullptr;
+    p.rows = (uint32_t)total; p.keys = a->keys; p.heads = a->heads; p.kv_heads = a->kv_heads;
+    p.back = a->back; p.ahead = a->ahead; p.kept_pages = 0; p.page_shift = 0; p.scale = a->scale;
+    p.status = nullptr;
+    p.seq_rows = a->rows;
+    p.past = a->keys >= a->rows ? a->keys - a->rows : 0;
+    p.max_position = p.past + a->rows - 1;
+    return flash_launch(p, a->q_dtype == TS_F32, stream, "flash");
 }

@@ -10,8 +10,8 @@
 // gfx950 design: HBM-bound byte moves. One group per (copy, buffer); each thread
 // moves 16-byte vectors, 256 threads cover 4 KiB per pass (a 16-row page of 8 kv
 // heads x 128 bf16 is 32 KiB: 8 passes, all loads of a pass issued before its
-// stores). Copies with a page or row count out of range are skipped and reported in
-// the status word.
+// stores). Copies with a page or row count out of range, or whose pages overlap
+// another copy's target, are skipped and reported in the status word.
 #include "common.h"
 #include "../../include/tessera_kv.h"
 
@@ -27,8 +27,16 @@ struct CopyParams {
 __global__ __launch_bounds__(256) void kv_copy_kernel(CopyParams p) {
     const uint32_t c = blockIdx.x / p.buffer_count, b = blockIdx.x % p.buffer_count;
     const ts_kv_copy cp = p.copies[c];
-    const bool bad = cp.from >= p.pages || cp.to >= p.pages || cp.rows > p.page ||
-                     (cp.from == cp.to && cp.rows > 0) || ((uintptr_t)p.buffers[b] & 15);
+    bool bad = cp.from >= p.pages || cp.to >= p.pages || cp.rows > p.page ||
+               (cp.from == cp.to && cp.rows > 0) || ((uintptr_t)p.buffers[b] & 15);
+    // Copies of one call run at once: a page another copy reads or writes may not be
+    // this copy's target, nor its source another's target (the result would depend
+    // on timing). Both copies of such a pair are skipped and reported.
+    for (uint32_t j = 0; j < p.copy_count; j++) {
+        if (j == c) continue;
+        const ts_kv_copy o = p.copies[j];
+        bad |= o.to == cp.to || o.from == cp.to || o.to == cp.from;
+    }
     if (bad || cp.rows == 0) {
         if (bad && threadIdx.x == 0 && p.status) atomicOr(p.status, TS_KV_STATUS_COPY);
         return;

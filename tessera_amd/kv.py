@@ -175,13 +175,21 @@ class Pool:
         return bool(self._l.tessera_kv_consistent(self._p))
 
 
-def copy_pages(buffers, copies, *, page, pages, status=None):
+def copy_pages(buffers, copies, *, page, pages, status=None, check=True):
     """Makes Pool.grow's copies on the device in every kept-row buffer (torch tensors
     [pages * page, ...], e.g. K and V of each layer), in stream order before the
-    launch that appends. copies: [(from, to, rows), ...]."""
+    launch that appends. copies: [(from, to, rows), ...]. check=False leaves the
+    overlap check to the device (which skips such copies and reports them)."""
     import torch
     if not copies:
         return
+    # The copies of one call run at once: no page may be one copy's target and another
+    # copy's source or target (the device skips and reports such pairs too).
+    for i, (f, t, _) in enumerate(copies if check else ()):
+        for j, (f2, t2, _) in enumerate(copies):
+            if i != j and (t == t2 or t == f2):
+                raise ValueError(f"copies {i} and {j} overlap: page {t} is written by one and read or written "
+                                 "by the other")
     dev = buffers[0].device
     ptrs = torch.tensor([b.data_ptr() for b in buffers], dtype=torch.int64).to(dev)
     raw = torch.tensor([[f, t, r & 0xFFFFFFFF, r >> 32] for f, t, r in copies], dtype=torch.int64)

@@ -292,6 +292,25 @@ def flash_rows(q, k, v, slots, positions, *, keys, scale, table=None, kept_pages
     return out
 
 
+MASKS = {"causal": lambda n: (abi.U32_MAX, 0, 1), "bidirectional": lambda n: (abi.U32_MAX, abi.U32_MAX, 0),
+         "within": lambda n: (n, n, 0), "back": lambda n: (n, 0, 1)}
+
+
+def flash(q, k, v, *, scale, mask="causal", n=0, out=None):
+    """Rule "flash" on whole sequences: q [seqs, rows, heads, 128] (f32 or bf16), k / v
+    [seqs, keys, kv_heads, 128] bf16, any mask of engine/ir/graph/src/node.rs:162-181
+    ("causal", "bidirectional", "within" n, "back" n)."""
+    seqs, rows, heads, width = q.shape
+    keys, kvh = k.shape[1], k.shape[2]
+    if out is None:
+        out = torch.empty((seqs, rows, heads, width), dtype=torch.float32, device=q.device)
+    back, ahead, causal = MASKS[mask](n)
+    a = abi.FlashArgs(_ptr(q), _ptr(k), _ptr(v), _ptr(out), seqs, rows, keys, heads, kvh, width, back, ahead,
+                      causal, scale, _DT[q.dtype], _DT[k.dtype], _DT[out.dtype])
+    abi.call("tessera_hip_flash", C.byref(a), _stream())
+    return out
+
+
 def rms_norm(x, gain, eps, out=None):
     rows, width = x.reshape(-1, x.shape[-1]).shape
     if out is None:

@@ -56,7 +56,7 @@ STRUCTS = {
     "ts_qk_args": "QkArgs", "ts_gather_args": "GatherArgs", "ts_take_args": "TakeArgs",
     "ts_softmax_args": "SoftmaxArgs", "ts_mix_args": "MixArgs", "ts_argmax_args": "ArgmaxArgs",
     "ts_keys_args": "KeysArgs", "ts_top_k_args": "TopKArgs", "ts_step_args": "StepArgs",
-    "ts_map_stage": "MapStage", "ts_after": "After", "ts_map_args": "MapArgs",
+    "ts_map_stage": "MapStage", "ts_after": "After", "ts_map_args": "MapArgs", "ts_flash_args": "FlashArgs",
 }
 # include/tessera_kv.h's structs and their bindings in tessera_amd/kv.py.
 KV_STRUCTS = {"ts_kv_run": "RunId", "ts_kv_copy": "PageCopy", "ts_kv_stats": "Stats", "ts_kv_copy_args": "CopyArgs"}

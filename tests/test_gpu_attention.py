@@ -351,3 +351,45 @@ def test_prefill_c3_full():
     pick = np.array(sorted(set(pick)))
     sub = dict(c, q=O.bf16_widen(qb[pick]), slots=c["slots"][pick], positions=c["positions"][pick])
     np.testing.assert_allclose(got[pick], want(sub, s), atol=4e-3, rtol=0)
+
+
+# attention_test.rs:44-60 flash_matches_cpu: (seqs, rows, keys) and the five masks.
+FLASH_CASES = [(1, 1, 1), (1, 1, 38), (2, 7, 7), (1, 33, 33), (2, 70, 93), (1, 128, 128), (2, 300, 300),
+               (1, 40, 20)]
+FLASH_MASKS = [("causal", 0), ("bidirectional", 0), ("within", 5), ("within", 40), ("back", 5)]
+
+
+@pytest.mark.parametrize("mask,n", FLASH_MASKS)
+@pytest.mark.parametrize("heads,kv_heads", [(2, 2), (16, 8)])
+def test_flash_whole_sequences_every_mask(mask, n, heads, kv_heads):
+    """Whole-sequence flash (tessera_hip_flash) against the oracle's attend over the
+    reference test's cases, f32 q, bf16 K/V. More rows than keys (1, 40, 20) is
+    refused for the causal masks, as interp refuses it; for the others the rows start
+    at position 0 and rows past every key's window write zeros."""
+    from tessera_amd import abi, rules as R
+    s = 1 / math.sqrt(128)
+    for seqs, rows, keys in FLASH_CASES:
+        r = rng(seqs * 1000 + rows * 10 + keys + heads)
+        q = r.standard_normal((seqs, rows, heads, 128)).astype(np.float32)
+        kb, kf = bf16_bits_normal(r, (seqs, keys, kv_heads, 128))
+        vb, vf = bf16_bits_normal(r, (seqs, keys, kv_heads, 128))
+        if keys < rows and mask in ("causal", "back"):
+            with pytest.raises(abi.HipError, match="causal mask"):
+                R.flash(to_dev(q, torch), to_dev(kb, torch), to_dev(vb, torch), scale=s, mask=mask, n=n)
+            continue
+        got = from_dev(R.flash(to_dev(q, torch), to_dev(kb, torch), to_dev(vb, torch), scale=s, mask=mask, n=n))
+        want = O.attend(q, kf, vf, s, mask, n)
+        np.testing.assert_allclose(got, want, atol=ATOL, rtol=0, err_msg=f"{(seqs, rows, keys)}")
+
+
+def test_flash_bf16_q_within_window():
+    """bf16 q (P once in bf16: 4e-3 as the ragged bf16-q case), a window both ways, 2
+    sequences of 1000 rows over 1200 keys."""
+    from tessera_amd import rules as R
+    r = rng(77)
+    s = 1 / math.sqrt(128)
+    qb, qf = bf16_bits_normal(r, (2, 1000, 16, 128))
+    kb, kf = bf16_bits_normal(r, (2, 1200, 8, 128))
+    vb, vf = bf16_bits_normal(r, (2, 1200, 8, 128))
+    got = from_dev(R.flash(to_dev(qb, torch), to_dev(kb, torch), to_dev(vb, torch), scale=s, mask="within", n=100))
+    np.testing.assert_allclose(got, O.attend(qf, kf, vf, s, "within", 100), atol=4e-3, rtol=0)

@@ -116,3 +116,19 @@ def test_copy_refuses_bad_pages():
     want = before.clone()
     want[6 * page: 6 * page + 3] = before[5 * page: 5 * page + 3]
     assert torch.equal(K, want)
+
+
+def test_copy_skips_overlapping_pages():
+    """Copies of one call run at once: a copy whose target another copy reads or writes
+    is skipped on the device with its partner, and reported; an unrelated copy runs."""
+    from tessera_amd import kv
+    page = 16
+    K = torch.arange(8 * page * 256, dtype=torch.int32, device="cuda").view(8 * page, 256)
+    before = K.clone()
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    kv.copy_pages([K], [(1, 2, 4), (2, 3, 4), (5, 6, 3)], page=page, pages=8, status=status, check=False)
+    torch.cuda.synchronize()
+    assert int(status.item()) == kv.STATUS_COPY
+    want = before.clone()
+    want[6 * page: 6 * page + 3] = before[5 * page: 5 * page + 3]
+    assert torch.equal(K, want)

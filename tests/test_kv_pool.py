@@ -119,3 +119,16 @@ def test_random_calls():
                 except PoolError:
                     assert pool.digest() == before
                 assert pool.consistent()
+
+
+def test_copy_pages_refuses_overlap_on_the_host():
+    """Two copies where one's target is the other's source (or target) are refused
+    before anything reaches a device."""
+    import pytest
+    torch = pytest.importorskip("torch")
+    from tessera_amd import kv
+    K = torch.zeros((8 * 16, 4), dtype=torch.int32)
+    with pytest.raises(ValueError, match="overlap"):
+        kv.copy_pages([K], [(1, 2, 4), (2, 3, 4)], page=16, pages=8)
+    with pytest.raises(ValueError, match="overlap"):
+        kv.copy_pages([K], [(1, 3, 4), (2, 3, 4)], page=16, pages=8)
