@@ -46,7 +46,11 @@ extern "C" {
  *   TS_INT4_G128  66 B a block: f16 scale, 128 nibbles (code - 8), 2q low, 2q+1 high
  * tessera_hip_lanes / tessera_hip_linear / tessera_hip_tiled accept them at any m. */
 enum { TS_F32 = 0, TS_BF16 = 1, TS_E4M3 = 2, TS_U32 = 3, TS_Q8_0 = 4, TS_MXFP8 = 5, TS_INT4_G32 = 6,
-       TS_Q4_0 = 7, TS_NVFP4 = 8, TS_MXFP4 = 9, TS_INT4_G128 = 10 };
+       TS_Q4_0 = 7, TS_NVFP4 = 8, TS_MXFP4 = 9, TS_INT4_G128 = 10, TS_F32_PARTS = 11 };
+/* TS_F32_PARTS: f32 weights as tessera_hip_pack_f32 lays them out, [2n, k] bf16: rows
+ * 0..n-1 the high parts bf16(w), rows n..2n-1 the low parts bf16(w - bf16(w)) (w to
+ * about 16 significant bits, every part exact on the matrix unit); the product sums
+ * x . hi + x . lo. Not with TS_AFTER_SILU_MUL, not for picked products. */
 
 /* Fused stages around a product (engine/plan/lower/src/kernels/map.rs:20-59 MapStage,
  * applied by `finish` at the store, map.rs:155-185). */
@@ -289,6 +293,17 @@ typedef struct {
     ts_after after;   /* by value */
 } ts_map_args;
 int tessera_hip_map(const ts_map_args *a, void *stream);
+
+/* f32 weights to the TS_F32_PARTS layout, once at load: out [2n, k] bf16 from w [n, k]
+ * f32 (high parts, then low parts; both round to nearest even).
+ * Replaces: the F32 form the reference's tiled / lanes rules read directly
+ * (engine/plan/codegen/src/form.rs:224-229), laid out for the matrix unit. */
+typedef struct {
+    const float *w;  /* [n, k] */
+    void *out;       /* [2n, k] bf16 */
+    uint32_t n, k;
+} ts_pack_args;
+int tessera_hip_pack_f32(const ts_pack_args *a, void *stream);
 
 /* ----------------------------------------------------------------------------
  * Whole-sequence attention with any mask (the reference's flash on the Attend site,

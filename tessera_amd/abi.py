@@ -25,6 +25,7 @@ TS_STATUS_POSITION = 1  # ts_rows_args.status: a row's position was refused
 TS_F32, TS_BF16, TS_E4M3, TS_U32 = 0, 1, 2, 3
 TS_Q8_0, TS_MXFP8, TS_INT4_G32, TS_Q4_0 = 4, 5, 6, 7  # block forms (engine/ir/mem/src/block.rs:251-291)
 TS_NVFP4, TS_MXFP4, TS_INT4_G128 = 8, 9, 10
+TS_F32_PARTS = 11  # f32 weights as tessera_hip_pack_f32 lays them out
 
 TS_AFTER_ADD = 1
 TS_AFTER_SILU_MUL = 2
@@ -126,6 +127,7 @@ KeysArgs = _args("KeysArgs", "ts_keys_args", [
     ("keys", _v), ("ids", _v), ("rows", _u), ("width", _u)])
 TopKArgs = _args("TopKArgs", "ts_top_k_args", [
     ("x", _v), ("ids", _v), ("rows", _u), ("width", _u), ("k", _u)])
+PackArgs = _args("PackArgs", "ts_pack_args", [("w", _v), ("out", _v), ("n", _u), ("k", _u)])
 FlashArgs = _args("FlashArgs", "ts_flash_args", [
     ("q", _v), ("k", _v), ("v", _v), ("out", _v), ("seqs", _u), ("rows", _u), ("keys", _u), ("heads", _u),
     ("kv_heads", _u), ("width", _u), ("back", _u), ("ahead", _u), ("causal", C.c_int32), ("scale", _f),
@@ -172,6 +174,7 @@ SIGNATURES = {
     "tessera_hip_top_k": (C.c_int, [C.POINTER(TopKArgs), _P]),
     "tessera_hip_map": (C.c_int, [C.POINTER(MapArgs), _P]),
     "tessera_hip_flash": (C.c_int, [C.POINTER(FlashArgs), _P]),
+    "tessera_hip_pack_f32": (C.c_int, [C.POINTER(PackArgs), _P]),
 }
 
 

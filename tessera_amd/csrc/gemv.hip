@@ -41,6 +41,7 @@ struct GemvParams {
     void *keys;  // TS_AFTER_ARGMAX: [m] uint64
     uint32_t waves;  // waves per group splitting k
     ts_after after;  // stage chain (count 0: none)
+    int pair_sum;    // TS_F32_PARTS: rows n.. are the low parts; the output sums the pair
 };
 
 namespace {
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
     constexpr int B = (B1 < B2 ? B1 : B2) > 0 ? (B1 < B2 ? B1 : B2) : 1;
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = p.waves;
     const uint32_t K = p.k, N = p.n, Mr = p.m;
-    const bool silu = p.stages & TS_AFTER_SILU_MUL, norm = p.stages & TS_BEFORE_RMS_NORM;
+    const bool silu = (p.stages & TS_AFTER_SILU_MUL) || p.pair_sum, norm = p.stages & TS_BEFORE_RMS_NORM;
     const uint32_t outs = silu ? R / 2 : R;
     const uint32_t o0 = blockIdx.x * outs;
 
@@ -273,7 +274,7 @@ __global__ __launch_bounds__(kMaxW * 64) void gemv_kernel(GemvParams p) {
         g *= pre_sg;
         u *= pre_su;
     }
-    float v = silu ? g / (1.0f + expf(-g)) * u : g;
+    float v = silu ? (p.pair_sum ? g + u : g / (1.0f + expf(-g)) * u) : g;
     if (p.stages & TS_AFTER_ADD) v += pre_a0;
     if (p.after.count && live) v = after_apply(p.after, v, (size_t)m * N + n);
     if (live) {
@@ -351,12 +352,12 @@ void gemv_plan(uint32_t n, uint32_t k, bool silu, bool w8, int *rows, uint32_t *
 int gemv_launch(const ts_linear_args *a, void *stream) {
     int r;
     uint32_t w, g;
-    const bool silu = a->stages & TS_AFTER_SILU_MUL;
+    const bool parts = a->w_dtype == TS_F32_PARTS, silu = (a->stages & TS_AFTER_SILU_MUL) || parts;
     gemv_plan(a->n, a->k, silu, a->w_dtype == TS_E4M3, &r, &w, &g);
     GemvParams p;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.gain = a->gain; p.a0 = a->a0;
     p.out = a->out; p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.eps = a->eps;
-    p.out_bf16 = a->out_dtype == TS_BF16; p.waves = w; p.keys = a->workspace;
+    p.out_bf16 = a->out_dtype == TS_BF16; p.waves = w; p.keys = a->workspace; p.pair_sum = parts;
     const int rc = linear_after(a, "lanes (gemv)", &p.after);
     if (rc) return rc;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;

@@ -40,6 +40,7 @@ struct LanesParams {
     float eps;
     int out_bf16;
     ts_after after;  // stage chain (count 0: none)
+    int pair_sum;    // TS_F32_PARTS: rows n.. are the low parts; the output sums the pair
 };
 
 // Raw weight bytes of one lane (row `row`, lane group g) for the 128-deep chunk at
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(kWaves * 64) void lanes_kernel(LanesParams p, float
                 g *= bf16_float(p.w_scale[n]);
                 if (SILU) u *= bf16_float(p.w_scale[N + n]);
             }
-            val[4 * t + r] = SILU ? silu(g) * u : g;
+            val[4 * t + r] = SILU ? (p.pair_sum ? g + u : silu(g) * u) : g;
         }
     // Value e: row 16 (e / 4) + 4 grp + e % 4.
     auto row_of = [&](int e) { return 16 * (uint32_t)(e / 4) + 4 * grp + (uint32_t)(e % 4); };
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(256) void lanes_finish(LanesParams p, const float *
         g *= bf16_float(p.w_scale[n]);
         if (SILU) u *= bf16_float(p.w_scale[N + n]);
     }
-    float v = SILU ? silu(g) * u : g;
+    float v = SILU ? (p.pair_sum ? g + u : silu(g) * u) : g;
     if (p.stages & TS_AFTER_ADD) v += p.a0[i];
     if (p.after.count) v = ts::after_apply(p.after, v, i);
     if (p.out_bf16) ((uint16_t *)p.out)[i] = bf16_bits(v);
@@ -405,7 +406,10 @@ int check(const ts_linear_args *a) {
     TS_REQUIRE(a->m >= 1 && a->m <= 64, "lanes: m=%u outside 1..64", a->m);
     TS_REQUIRE(a->n >= 1 && a->k >= 1, "lanes: empty product n=%u k=%u", a->n, a->k);
     TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "lanes: x dtype %d", a->x_dtype);
-    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3, "lanes: w dtype %d", a->w_dtype);
+    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3 || a->w_dtype == TS_F32_PARTS,
+               "lanes: w dtype %d (f32 weights: pack them with tessera_hip_pack_f32, TS_F32_PARTS)", a->w_dtype);
+    TS_REQUIRE(a->w_dtype != TS_F32_PARTS || !(a->stages & TS_AFTER_SILU_MUL),
+               "lanes: TS_F32_PARTS weights with TS_AFTER_SILU_MUL");
     TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "lanes: out dtype %d", a->out_dtype);
     TS_REQUIRE(a->w_dtype != TS_E4M3 || a->w_scale, "lanes: e4m3 weights need w_scale");
     TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "lanes: TS_AFTER_ADD needs a0");
@@ -430,7 +434,7 @@ extern "C" size_t tessera_hip_lanes_workspace(const ts_linear_args *a) {
     if (!a || a->m <= 4 || a->m > 64 || ts::block_form(a->w_dtype)) return 0;
     const Plan pl = plan(a);
     if (pl.splits <= 1) return 0;
-    const size_t per = (size_t)a->m * a->n * ((a->stages & TS_AFTER_SILU_MUL) ? 2 : 1);
+    const size_t per = (size_t)a->m * a->n * ((a->stages & TS_AFTER_SILU_MUL) || a->w_dtype == TS_F32_PARTS ? 2 : 1);
     return (size_t)pl.splits * per * sizeof(float);
 }
 
@@ -454,7 +458,9 @@ extern "C" int tessera_hip_lanes(const ts_linear_args *a, void *stream) {
     p.out_bf16 = a->out_dtype == TS_BF16;
     rc = ts::linear_after(a, "lanes", &p.after);
     if (rc) return rc;
-    const bool silu = a->stages & TS_AFTER_SILU_MUL, norm = a->stages & TS_BEFORE_RMS_NORM;
+    const bool parts = a->w_dtype == TS_F32_PARTS;
+    const bool silu = (a->stages & TS_AFTER_SILU_MUL) || parts, norm = a->stages & TS_BEFORE_RMS_NORM;
+    p.pair_sum = parts;
     const bool xf = a->x_dtype == TS_F32, w8 = a->w_dtype == TS_E4M3;
     const uint32_t mt = (a->m + 15) / 16;
     const bool chain = p.after.count;

@@ -96,3 +96,30 @@ extern "C" int tessera_hip_map(const ts_map_args *a, void *stream) {
     TS_CHECK_LAUNCH("map launch");
     return TS_OK;
 }
+
+namespace ts {
+namespace {
+
+// hi = bf16(w), lo = bf16(w - hi), both round to nearest even (NaN kept quiet).
+__global__ __launch_bounds__(256) void pack_f32_kernel(const float *w, uint16_t *out, uint64_t count) {
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < count; i += (uint64_t)gridDim.x * 256) {
+        const float v = w[i];
+        const uint16_t hi = bf16_bits(v);
+        out[i] = hi;
+        out[count + i] = bf16_bits(v - bf16_float(hi));
+    }
+}
+
+}  // namespace
+}  // namespace ts
+
+extern "C" int tessera_hip_pack_f32(const ts_pack_args *a, void *stream) {
+    TS_REQUIRE(a && a->w && a->out, "pack_f32: null pointer");
+    const uint64_t count = (uint64_t)a->n * a->k;
+    if (count == 0) return TS_OK;
+    const uint32_t groups = (uint32_t)std::min<uint64_t>((count + 255) / 256, 8192);
+    hipLaunchKernelGGL(ts::pack_f32_kernel, dim3(groups), dim3(256), 0, (hipStream_t)stream, a->w,
+                       (uint16_t *)a->out, count);
+    TS_CHECK_LAUNCH("pack_f32 launch");
+    return TS_OK;
+}

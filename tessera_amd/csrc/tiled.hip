@@ -50,6 +50,7 @@ struct TiledParams {
     const uint32_t *perm, *row_start, *tile_start;
     uint32_t matrices, repeat, stride, offset;
     ts_after after;  // stage chain (count 0: none)
+    int pair_sum;    // TS_F32_PARTS: the second row block is the low parts; the output sums the pair
 };
 
 // Byte offset of (row, chunk) in a swizzled [rows][8 chunks of 16B] tile.
@@ -244,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void tiled_kernel(TiledParams p) {
                         g *= bf16_float(scale[min(n + r, N - 1)]);
                         u *= bf16_float(scale[N + min(n + r, N - 1)]);
                     }
-                    val[i][j][r] = g / (1.0f + expf(-g)) * u;
+                    val[i][j][r] = p.pair_sum ? g + u : g / (1.0f + expf(-g)) * u;
                 } else {
                     if (W8) g *= bf16_float(scale[min(n + r, N - 1)]);
                     val[i][j][r] = g;
@@ -511,7 +512,8 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
     const uint32_t N = p.n;
     auto value = [&](int i, int j, int r) {
         const float g = acc[i][j][r];
-        return SILU ? g / (1.0f + expf(-g)) * acc[i][j + P::FJ / 2][r] : g;
+        const float u = SILU ? acc[i][j + P::FJ / 2][r] : 0.0f;
+        return SILU ? (p.pair_sum ? g + u : g / (1.0f + expf(-g)) * u) : g;
     };
     constexpr int JO = SILU ? P::FJ / 2 : P::FJ;
     constexpr uint32_t WO = SILU ? P::WN / 2 : P::WN;
@@ -664,7 +666,10 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TS_REQUIRE(a->m >= 1 && a->n >= 1 && a->k >= 1, "tiled: empty product m=%u n=%u k=%u", a->m, a->n, a->k);
     TS_REQUIRE(a->k % 8 == 0, "tiled: k=%u must be a multiple of 8", a->k);
     TS_REQUIRE(a->x_dtype == TS_F32 || a->x_dtype == TS_BF16, "tiled: x dtype %d", a->x_dtype);
-    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3, "tiled: w dtype %d", a->w_dtype);
+    TS_REQUIRE(a->w_dtype == TS_BF16 || a->w_dtype == TS_E4M3 || a->w_dtype == TS_F32_PARTS,
+               "tiled: w dtype %d (f32 weights: pack them with tessera_hip_pack_f32, TS_F32_PARTS)", a->w_dtype);
+    TS_REQUIRE(a->w_dtype != TS_F32_PARTS || !(a->stages & TS_AFTER_SILU_MUL),
+               "tiled: TS_F32_PARTS weights with TS_AFTER_SILU_MUL");
     TS_REQUIRE(a->out_dtype == TS_F32 || a->out_dtype == TS_BF16, "tiled: out dtype %d", a->out_dtype);
     TS_REQUIRE(a->w_dtype != TS_E4M3 || a->w_scale, "tiled: e4m3 weights need w_scale");
     TS_REQUIRE(!(a->stages & TS_AFTER_ADD) || a->a0, "tiled: TS_AFTER_ADD needs a0");
@@ -677,7 +682,11 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     if (rc) return rc;
     const int big = ts::tiled_big_launch(a, stream);
     if (big != 1) return big;
-    const bool silu = a->stages & TS_AFTER_SILU_MUL;
+    // f32 weights as two bf16 parts run as a pair of row blocks, summed at the store.
+    const bool parts = a->w_dtype == TS_F32_PARTS;
+    const bool silu = (a->stages & TS_AFTER_SILU_MUL) || parts;
+    const int32_t w_dtype = parts ? TS_BF16 : a->w_dtype;
+    p.pair_sum = parts;
     p.x = a->x; p.w = a->w; p.w_scale = (const uint16_t *)a->w_scale; p.a0 = a->a0; p.out = a->out;
     p.m = a->m; p.n = a->n; p.k = a->k; p.stages = a->stages; p.out_bf16 = a->out_dtype == TS_BF16;
     // 64x64 tiles when 128x128 would give fewer than 2 groups per CU: more groups to
@@ -690,7 +699,7 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
     TS_REQUIRE(gy <= 65535, "tiled: m=%u too large for one launch", a->m);
     p.perm = p.row_start = p.tile_start = nullptr;
     p.matrices = 0; p.repeat = 1; p.stride = 0; p.offset = 0;
-    if (pipe_fits(a->x_dtype, a->w_dtype, a->m, a->k, silu ? 2 * a->n : a->n)) {
+    if (pipe_fits(a->x_dtype, w_dtype, a->m, a->k, silu ? 2 * a->n : a->n)) {
         // 128 x 128 tiles from one tile per CU up (fewer, larger tiles read less per
         // flop), 64 x 64 below that (measured on the 2048-row projections: q with 256
         // tiles of 128 runs 1.15x faster than with 1024 of 64; o, kv and down with 128
@@ -702,8 +711,8 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
         return pipe_launch<64, 64, 64, 4, false>(p, silu, stream);
     }
     const bool chain = p.after.count;
-    Kern k = bt == 64 ? pick_kernel<64, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu, chain)
-                      : pick_kernel<128, false>(a->x_dtype == TS_F32, a->w_dtype == TS_E4M3, silu, chain);
+    Kern k = bt == 64 ? pick_kernel<64, false>(a->x_dtype == TS_F32, w_dtype == TS_E4M3, silu, chain)
+                      : pick_kernel<128, false>(a->x_dtype == TS_F32, w_dtype == TS_E4M3, silu, chain);
     hipLaunchKernelGGL(k, dim3(gx, gy), dim3(kThreads), 0, (hipStream_t)stream, p);
     TS_CHECK_LAUNCH("tiled launch");
     return TS_OK;
@@ -748,6 +757,7 @@ extern "C" int tessera_hip_picked(const ts_picked_args *a, void *stream) {
     if (rc) return rc;
     const bool silu = a->stages & TS_AFTER_SILU_MUL;
     TiledParams p;
+    p.pair_sum = 0;
     ts::after_check(a->after, true, "picked", &p.after);
     rc = ts::zero_absent_launch(route, a->count, a->out, a->n, a->out_dtype == TS_BF16, p.after, stream);
     if (rc) return rc;

@@ -97,7 +97,8 @@ def linear_args(x, w, out, *, w_scale=None, gain=None, a0=None, stages=0, eps=1e
     a.m, a.n, a.k = m, n, k
     a.x_dtype, a.out_dtype = _DT[x.dtype], _DT[out.dtype]
     # Block forms: w is the packed tensor (uint8: head, then each row's blocks).
-    a.w_dtype = BLOCK_FORMS[w_form] if w_form is not None else _DT[w.dtype]
+    a.w_dtype = (abi.TS_F32_PARTS if w_form == "f32_parts" else BLOCK_FORMS[w_form]) if w_form is not None \
+        else _DT[w.dtype]
     a.stages, a.eps = stages, eps
     return a
 
@@ -107,10 +108,10 @@ def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, g
     """rows: the weight rows of a packed block-form tensor (w is then flat bytes).
     after: a chain() run on each sum before the store."""
     m = x.shape[0]
-    wr = rows if w_form is not None else w.shape[0]
+    wr = rows if w_form is not None and w_form != "f32_parts" else w.shape[0]
     if wr is None:
         raise ValueError("a block-form weight tensor needs rows=")
-    n = wr // 2 if silu_mul else wr
+    n = wr // 2 if silu_mul or w_form == "f32_parts" else wr
     if out is None:
         out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     stages = (abi.TS_AFTER_ADD if a0 is not None else 0) | (abi.TS_AFTER_SILU_MUL if silu_mul else 0) | \
@@ -122,6 +123,15 @@ def _linear(fn: str, x, w, *, out=None, out_dtype=torch.float32, w_scale=None, g
     need = getattr(lib, fn + "_workspace")(C.byref(a)) if hasattr(lib, fn + "_workspace") else 0
     a.workspace, a.workspace_bytes = workspace(x.device).get(need)
     abi.call(fn, C.byref(a), _stream())
+    return out
+
+
+def pack_f32(w):
+    """f32 weights [n, k] to the TS_F32_PARTS layout ([2n, k] bf16: high parts, then
+    low parts), once at load; pass the result with w_form="f32_parts"."""
+    n, k = w.shape
+    out = torch.empty((2 * n, k), dtype=torch.bfloat16, device=w.device)
+    abi.call("tessera_hip_pack_f32", C.byref(abi.PackArgs(_ptr(w), _ptr(out), n, k)), _stream())
     return out
 
 

@@ -57,6 +57,7 @@ STRUCTS = {
     "ts_softmax_args": "SoftmaxArgs", "ts_mix_args": "MixArgs", "ts_argmax_args": "ArgmaxArgs",
     "ts_keys_args": "KeysArgs", "ts_top_k_args": "TopKArgs", "ts_step_args": "StepArgs",
     "ts_map_stage": "MapStage", "ts_after": "After", "ts_map_args": "MapArgs", "ts_flash_args": "FlashArgs",
+    "ts_pack_args": "PackArgs",
 }
 # include/tessera_kv.h's structs and their bindings in tessera_amd/kv.py.
 KV_STRUCTS = {"ts_kv_run": "RunId", "ts_kv_copy": "PageCopy", "ts_kv_stats": "Stats", "ts_kv_copy_args": "CopyArgs"}
@@ -157,7 +158,7 @@ def test_dtype_enum_matches_header():
     assert pairs == {"TS_F32": abi.TS_F32, "TS_BF16": abi.TS_BF16, "TS_E4M3": abi.TS_E4M3, "TS_U32": abi.TS_U32,
                      "TS_Q8_0": abi.TS_Q8_0, "TS_MXFP8": abi.TS_MXFP8, "TS_INT4_G32": abi.TS_INT4_G32,
                      "TS_Q4_0": abi.TS_Q4_0, "TS_NVFP4": abi.TS_NVFP4, "TS_MXFP4": abi.TS_MXFP4,
-                     "TS_INT4_G128": abi.TS_INT4_G128}
+                     "TS_INT4_G128": abi.TS_INT4_G128, "TS_F32_PARTS": abi.TS_F32_PARTS}
 
 
 def test_flash_rows_refuses_more_row_groups_than_its_order_packs():

@@ -265,3 +265,35 @@ def test_bf16_output_rounding_matches_oracle():
     assert bad.size == 0, "x bits / got / want: " + ", ".join(
         f"{vals[i:i + 1].view(np.uint32)[0]:08x}/{got[i]:04x}/{want[i]:04x}" for i in bad[:12]) + f" ({bad.size} differ)"
     assert np.all((got[nan] & 0x7fff) > 0x7f80)
+
+
+@pytest.mark.parametrize("m,n,k", SHAPES + [(128, 1024, 1024), (2048, 1024, 256)])
+@pytest.mark.parametrize("xdt", ["f32", "bf16"])
+def test_linear_f32_weights(m, n, k, xdt):
+    """f32 weights (tiles_match_cpu iterates every float form, engine/rules/linear/tests/
+    common/mod.rs:67-75): packed once into two bf16 parts (tessera_hip_pack_f32, checked
+    bit for bit here), then the product of every kernel family against the oracle's
+    f32 product, within the analytic bound with ew = |w| 2^-16 and four part products
+    per output."""
+    R = _rules()
+    r = rng(300 + m + n + k)
+    w = (r.standard_normal((n, k)) * 0.05).astype(np.float32)
+    wd = to_dev(w, torch)
+    packed = R.pack_f32(wd)
+    hi = O.bf16_narrow(w)
+    lo = O.bf16_narrow(w - O.bf16_widen(hi))
+    assert np.array_equal(packed.view(torch.int16).cpu().numpy().view(np.uint16), np.concatenate([hi, lo]))
+    if xdt == "f32":
+        x = r.standard_normal((m, k)).astype(np.float32)
+        xd = to_dev(x, torch)
+    else:
+        xb, x = bf16_bits_normal(r, (m, k))
+        xd = to_dev(xb, torch)
+    if m * n * k > 1 << 28:
+        O.set_threads(O.lib().or_threads_available())
+    want = O.product(x, w)
+    O.set_threads(1)
+    got = from_dev(R.linear(xd, packed, w_form="f32_parts"))
+    from tests.helpers import product_bound
+    bound = product_bound(x, w, x_bits=16 if xdt == "f32" else None, parts=4, w_bits=16, lane=9)
+    _check(got, want, bound)
