@@ -81,8 +81,17 @@ TS_DEV uint64_t key_row(const FlashParams &p, uint32_t slot, uint32_t pos, const
 typedef __attribute__((address_space(3))) void flash_lds_void;
 
 // Bytes of one key block buffer in LDS: 64 K rows then 64 V rows of 256 bytes, the
-// 16-byte chunks of row key at chunk ^ (key & 15).
+// 16-byte chunks of row key at chunk ^ kswz(key).
 constexpr uint32_t kBlockBytes = 2 * kKeys * 256;
+
+// The chunk swizzle of a key row: a permutation of the key's low four bits (bits 0, 1
+// to 2, 3; bit 2 to 1; bit 3 to 0). K fragment reads (16 keys of one chunk) see 16
+// distinct slots because it is one-to-one; the transposing V reads (4 consecutive
+// keys of one 16-lane block, chunks 2d and 2d + 1) see 8 distinct slots in each block
+// and 16 across two blocks, where XOR by key & 15 put two keys on one bank.
+TS_DEV uint32_t kswz(uint32_t key) {
+    return ((key & 3) << 2) | (((key >> 2) & 1) << 1) | ((key >> 3) & 1);
+}
 
 // Sums and maxima over the four 16-lane rows of a wave, in every lane (gfx950
 // permlane swaps: VALU).
@@ -329,7 +338,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
     // (keys 32 st + 4 grp + col / 4 and + 16, d 16 d + 4 (col & 3)).
     uint32_t koff[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) koff[j] = col * 256 + (((4 * grp + j) ^ col) << 4);
+    for (int j = 0; j < 4; j++) koff[j] = col * 256 + (((4 * grp + j) ^ kswz(col)) << 4);
     const uint32_t vk = 4 * grp + (col >> 2), vbase = vk * 256 + 8 * (col & 1), vc = (col & 3) >> 1;
 
     float m[kQT], l[kQT];
@@ -369,7 +378,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
         char *base = kv_lds + buf * kBlockBytes;
 #pragma unroll
         for (int c = 0; c < kNI; c++) {
-            const uint32_t sg = c * kWaves + wave, key = 4 * sg + (lane >> 4), chunk = (lane & 15) ^ (key & 15);
+            const uint32_t sg = c * kWaves + wave, key = 4 * sg + (lane >> 4), chunk = (lane & 15) ^ kswz(key & 15);
             const uint64_t row = key_row(p, slot, min(kb + key, hi), stab, p0);
             const size_t e = (row * p.kv_heads + kvh) * 128 + chunk * 8;
             __builtin_amdgcn_global_load_lds((const void *)(p.k + e), (flash_lds_void *)(base + sg * 1024), 16, 0, 0);
@@ -491,7 +500,7 @@ __global__ __launch_bounds__(256 * HG) void flash_rows_kernel(FlashParams p) {
             for (int st = 0; st < 2; st++) {
                 // Positions 8 grp .. + 3 and + 4 .. + 7 of step st hold keys
                 // 32 st + 4 grp + i and 32 st + 16 + 4 grp + i (P^T's order).
-                const char *va_at = vbuf + vbase + (((2 * d + vc) ^ vk) << 4) + 32 * st * 256;
+                const char *va_at = vbuf + vbase + (((2 * d + vc) ^ kswz(vk)) << 4) + 32 * st * 256;
                 const u32x2 va = read_vt4(va_at), vb = read_vt4(va_at + 16 * 256);
                 const bf16x8 vf = as_bf16x8(u32x4{va.x, va.y, vb.x, vb.y});
 #pragma unroll
