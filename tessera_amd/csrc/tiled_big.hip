@@ -125,6 +125,9 @@ TS_DEV bool tile_of(const BigParams &p, uint32_t b, uint32_t &m0, uint32_t &n0) 
     return n0 < p.n;
 }
 
+#ifndef TS_BIG_MIN_TILES
+#define TS_BIG_MIN_TILES 240
+#endif
 #ifndef TS_BIG_STAGGER
 #define TS_BIG_STAGGER 5
 #endif
@@ -282,7 +285,7 @@ int tiled_big_launch(const ts_linear_args *a, void *stream) {
     if (a->after) return 1;
     if (a->k % BK != 0) return 1;  // whole 64-deep steps: loads go straight to LDS, no zero fill
     const uint32_t gx = (a->n + BN - 1) / BN, gy = (a->m + BM - 1) / BM;
-    if ((uint64_t)gx * gy < 240 || gy > 65535) return 1;
+    if ((uint64_t)gx * gy < TS_BIG_MIN_TILES || gy > 65535) return 1;
     // 128 KiB of dynamic LDS needs the function attribute raised once per process.
     static const hipError_t attr =
         hipFuncSetAttribute((const void *)tiled_big_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kLds);
