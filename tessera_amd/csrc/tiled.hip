@@ -31,6 +31,9 @@
 
 namespace {
 
+#ifndef TS_PIPE_WIDE
+#define TS_PIPE_WIDE 1
+#endif
 constexpr int BM = 128, BN = 128, BK = 64;  // the default tile; BT = 64 for products with few tiles
 constexpr int kThreads = 256;
 
@@ -522,6 +525,11 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
         // XOR-swizzled by row), then whole 16-byte chunks of rows to memory.
         constexpr uint32_t CH = OC / 8;  // chunks per output row
         static_assert(TM * OC * 2 <= P::LDS, "pipe epilogue fits the stages");
+        // Chunk c of row r: XOR by the row when CH is a power of two, else rotated by
+        // the row (an XOR could leave the row).
+        auto slot = [](uint32_t r, uint32_t c) {
+            return (CH & (CH - 1)) == 0 ? c ^ (r % CH) : (c + r) % CH;
+        };
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int i = 0; i < P::FI; i++) {
@@ -529,7 +537,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
 #pragma unroll
             for (int j = 0; j < JO; j++) {
                 const uint32_t c = wn * WO + j * 16 + 4 * grp;
-                *(u32x2 *)(lds + r * OC * 2 + ((((c >> 3) ^ (r % CH))) << 4) + (c & 7) * 2) =
+                *(u32x2 *)(lds + r * OC * 2 + (slot(r, c >> 3) << 4) + (c & 7) * 2) =
                     u32x2{pack_bf16x2(value(i, j, 0), value(i, j, 1)), pack_bf16x2(value(i, j, 2), value(i, j, 3))};
             }
         }
@@ -540,7 +548,7 @@ __global__ __launch_bounds__(kThreads, 2) void tiled_pipe_kernel(TiledParams p) 
             const uint32_t r = f / CH, c = f % CH;
             const uint32_t m = m0 + r, n = n0 + c * 8;
             if (m >= p.m || n >= N) continue;
-            const u32x4 v = *(const u32x4 *)(lds + r * OC * 2 + ((c ^ (r % CH)) << 4));
+            const u32x4 v = *(const u32x4 *)(lds + r * OC * 2 + (slot(r, c) << 4));
             uint16_t *o = (uint16_t *)p.out + (size_t)m * N + n;
             if (rows16 && n + 8 <= N) {
                 *(u32x4 *)o = v;
@@ -706,8 +714,16 @@ extern "C" int tessera_hip_tiled(const ts_linear_args *a, void *stream) {
         // tiles of 128 run 1.4-1.5x slower than with 512 of 64).
         const uint64_t oc = silu ? 64 : 128;
         const uint64_t tiles = (a->n + oc - 1) / oc * ((a->m + 127) / 128);
+        // 128 x 192 when that fills the 512 group slots (two groups a CU) in fewer
+        // rounds of equal work than 128 x 128 does (the C2 gate_up: 768 tiles of 128,
+        // a round and a half, against 512 of 192).
+        const uint64_t tiles192 = (a->n + oc * 3 / 2 - 1) / (oc * 3 / 2) * ((a->m + 127) / 128);
+        const bool wide = ((tiles192 + 511) / 512) * 3 < ((tiles + 511) / 512) * 2;
         // A stage chain takes 64 x 64 tiles: at 128 x 128 its values and sums spill.
-        if (tiles >= 256 && !p.after.count) return pipe_launch<128, 128, 64, 2, false>(p, silu, stream);
+        if (tiles >= 256 && !p.after.count) {
+            if (wide && TS_PIPE_WIDE) return pipe_launch<128, 192, 64, 2, false>(p, silu, stream);
+            return pipe_launch<128, 128, 64, 2, false>(p, silu, stream);
+        }
         return pipe_launch<64, 64, 64, 4, false>(p, silu, stream);
     }
     const bool chain = p.after.count;
