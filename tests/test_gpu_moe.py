@@ -49,6 +49,7 @@ def _picked_want(x, table_bits, ids, repeat, first, offset, n, silu):
     (600, 16, 128, 130, 4, 2, "bf16"),   # ids below `first` and past the set read zeros
     (2000, 64, 64, 64, 8, 0, "bf16"),
     (1000, 330, 64, 32, 1, 0, "bf16"),  # more matrices than the one-pass routing scan takes
+    (700, 8, 128, 192, 2, 0, "bf16"),    # columns in whole 192-wide tiles: the 128 x 192 form
 ])
 def test_picked_matches_oracle(rows, count, k, n, repeat, first, xdt):
     R = _rules()
@@ -147,7 +148,8 @@ def test_take_softmax_mix():
     assert np.allclose(from_dev(R.softmax(to_dev(rows2, torch))), want2, atol=1e-6)
 
 
-@pytest.mark.parametrize("tokens,hidden,experts,top,ffn", [(384, 256, 16, 4, 128), (1024, 1024, 128, 8, 512)])
+@pytest.mark.parametrize("tokens,hidden,experts,top,ffn", [(384, 256, 16, 4, 128), (1024, 1024, 128, 8, 512),
+                                                         (512, 512, 32, 4, 192)])  # gate/up in 128 x 192 tiles
 def test_moe_layer_matches_oracle(tokens, hidden, experts, top, ffn):
     """One MoE MLP (decoder.rs:73-84) plus a shared expert: a small shape, and C5's
     128 experts top-8 at 1024 tokens (hidden and FFN narrowed so the oracle is quick)."""
