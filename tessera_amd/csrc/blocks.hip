@@ -236,8 +236,9 @@ typedef __attribute__((address_space(3))) void block_lds_void;
 constexpr uint32_t kShortBytes = 9200;  // LDS bytes of one wave's rows (short form; staged in 9 KiB + a word)
 
 // Passes a wave of the short form with L lanes a row (64 / L rows a pass): 16 rows a
-// wave, 8 at L = 32, so the rows' bytes fit kShortBytes. short_pick also takes 2 passes
-// at L = 32 for rows too wide for 4, and 4 passes at L = 8 for 128-code blocks.
+// wave, 8 at L = 32, so the rows' bytes fit kShortBytes. short_pick also takes 4 passes
+// of 2 rows in twice the stage (or 2 passes) at L = 32 for rows too wide for 4 passes of
+// 2 in one stage, and 4 passes at L = 8 for 128-code blocks.
 constexpr int short_np(int L) { return L == 32 ? 4 : L == 16 ? 4 : 2; }
 
 // Short rows (at most 32 blocks, e.g. 1024 codes of 32-code blocks, or of 128-code
@@ -356,7 +357,14 @@ ShortKern short_pick(uint32_t m, bool xf, uint32_t nb, uint32_t *rows) {
     if (nb > 32) return nullptr;
     *rows = (64 / L) * short_np(L);
     if ((uint64_t)*rows * nb * BF::BB > kShortBytes) {
-        // Wide blocks (128 codes): 2 passes of 2 rows at L = 32 (4 rows a wave).
+        // Wide blocks (128 codes) at L = 32: 4 passes of 2 rows (8 rows a wave in twice
+        // the stage, four chains a lane: 14336 x 4096 int4_g128 18.0 -> 13.2 us), else 2
+        // passes (4 rows a wave). (8 passes of the 32-code forms' rows measured slower:
+        // half the waves.)
+        if (L == 32 && (uint64_t)8 * nb * BF::BB <= 2 * kShortBytes) {
+            *rows = 8;
+            return xf ? short_m<F, true, 32, 4, 2 * kShortBytes>(m) : short_m<F, false, 32, 4, 2 * kShortBytes>(m);
+        }
         *rows = 4;
         if (L == 32 && (uint64_t)4 * nb * BF::BB <= kShortBytes)
             return xf ? short_m<F, true, 32, 2>(m) : short_m<F, false, 32, 2>(m);
