@@ -388,7 +388,11 @@ __global__ __launch_bounds__(kMaxWaves * 64) void attend_rows_kernel(RowsParams 
 // group's page-table entries are copied to LDS once; a group whose keys all lie
 // outside the row's range writes an empty partial and leaves without loading.
 // Same per-block math and partial layout as attend_rows_kernel.
-constexpr int kLongWaves = 8;
+// Two waves a group and about sixteen groups a (row, kv head) at the C3 decode shape:
+// 121-123 us against 130-131 with 8 waves and four groups, the same keys a wave
+// (smaller groups spread the ragged rows' work over the CUs more evenly; 1 wave and
+// 32 groups 127, 4 waves and 8 groups 124-126).
+constexpr int kLongWaves = 2;
 constexpr uint32_t kLongPages = 1024;  // page-table entries a group keeps in LDS
 
 template <int G>
@@ -666,9 +670,9 @@ Split split(const ts_rows_args *a, bool step) {
     if (step && s.waves < G + 2) s.waves = (G + 2) < max_waves ? G + 2 : max_waves;
     s.iters = 0;
     if (!step && span > kLongSpan && G <= 4) {
-        // Long contexts: each wave streams iters x 32 keys, a group 8 waves of them;
-        // about a quarter of the longest span per group keeps ~4 groups per (row, kv head).
-        s.iters = std::max(1u, std::min(32u, span / (4 * kLongWaves * 32)));
+        // Long contexts: each wave streams iters x 32 keys (iters ~ span / 1024), a
+        // group kLongWaves waves of them: ~16 groups per (row, kv head).
+        s.iters = std::max(1u, std::min(32u, span / (16 * kLongWaves * 32)));
         s.wave_keys = 32;
         s.waves = kLongWaves;
         s.parts = (span + kLongWaves * 32 * s.iters - 1) / (kLongWaves * 32 * s.iters);

@@ -13,7 +13,7 @@ import ctypes as C
 
 import numpy as np
 
-LONG_WAVES, LONG_PAGES, LONG_SPAN = 8, 1024, 2048
+LONG_WAVES, LONG_PAGES, LONG_SPAN = 2, 1024, 2048
 G_STRIDE = 130  # floats of one (max, sum, 128 acc) partial
 
 
@@ -29,8 +29,8 @@ def c3_decode_case():
 
 
 def library_split_iters(span):
-    """split() of attention.hip for the long kernel: iters = clamp(span / (4 * 8 * 32), 1, 32)."""
-    return max(1, min(32, span // (4 * LONG_WAVES * 32)))
+    """split() of attention.hip for the long kernel: iters = clamp(span / (16 * 2 * 32), 1, 32)."""
+    return max(1, min(32, span // (16 * LONG_WAVES * 32)))
 
 
 def model(case, iters, workspace_floats):
