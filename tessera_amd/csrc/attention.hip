@@ -615,6 +615,33 @@ __global__ __launch_bounds__(256) void attend_rows_merge(RowsParams p, uint32_t 
     const float *all = p.partials + gi * parts * G * 130;
     for (uint32_t e = threadIdx.x; e < G * 128; e += blockDim.x) {
         const uint32_t h = e / 128, d = e % 128;
+        // Up to 16 partitions: every (m, l, o) loaded at once, one round trip (the same
+        // max and the same sums in partition order as the batched loop below).
+        constexpr uint32_t kOne = 16;
+        if (parts <= kOne) {
+            float mq[kOne], lq[kOne], oq[kOne];
+#pragma unroll
+            for (uint32_t j = 0; j < kOne; j++) {
+                const float *pq = all + (min(j, parts - 1) * G + h) * 130;  // clamped: read, not used
+                mq[j] = pq[0];
+                lq[j] = pq[1];
+                oq[j] = pq[2 + d];
+            }
+            float M = -INFINITY;
+#pragma unroll
+            for (uint32_t j = 0; j < kOne; j++)
+                if (j < parts) M = fmaxf(M, mq[j]);
+            float L = 0.0f, O = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < kOne; j++)
+                if (j < parts) {
+                    const float f = (mq[j] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mq[j] - M);
+                    L += lq[j] * f;
+                    O += oq[j] * f;
+                }
+            p.out[((size_t)r * p.heads + kvh * G + h) * 128 + d] = O / L;
+            continue;
+        }
         // Partitions in batches of 8 with every load of a batch issued before use
         // (clamped indices are read, not used); sums stay in partition order.
         constexpr uint32_t kB = 8;
