@@ -1,8 +1,9 @@
 """A CPU model of attend_long_kernel's address arithmetic (tessera_amd/csrc/attention.hip),
 run over the C3 decode inputs (32 rows, contexts U[512, 8192] seed 2, 16 q / 8 kv heads,
-16-row pages in a shuffled table) at the split the library picks and at every pinned
-iteration count 1..32: every page-table read, LDS table index, kept-row load, partial
-write and merge read must land inside its buffer.
+16-row pages in a shuffled table) at the split the library picks (groups of 2 waves) and
+at every pinned iteration count 1..32, for groups of 2 waves and of 8 (the earlier form):
+every page-table read, LDS table index, kept-row load, partial write and merge read must
+land inside its buffer.
 
 This guards the conclusion that the long-context kernel's accesses are in bounds for
 every iteration count (one such pinned count once ran on a GPU together with a
@@ -13,7 +14,7 @@ import ctypes as C
 
 import numpy as np
 
-LONG_WAVES, LONG_PAGES, LONG_SPAN = 2, 1024, 2048
+LONG_WAVES, LONG_PAGES, LONG_SPAN = 2, 1024, 2048  # waves a group as built
 G_STRIDE = 130  # floats of one (max, sum, 128 acc) partial
 
 
@@ -33,14 +34,14 @@ def library_split_iters(span):
     return max(1, min(32, span // (16 * LONG_WAVES * 32)))
 
 
-def model(case, iters, workspace_floats):
+def model(case, iters, workspace_floats, waves=LONG_WAVES):
     pos, slots = case["pos"], case["slots"]
     shift = int(np.log2(case["page"]))
     pmask = case["page"] - 1
     kvh_n, G = case["kv_heads"], case["heads"] // case["kv_heads"]
     kept_pages, table, total_rows = case["kept_pages"], case["table"], case["total_rows"]
     span = int(pos.max()) + 1
-    span_keys = LONG_WAVES * 32 * iters
+    span_keys = waves * 32 * iters
     parts = (span + span_keys - 1) // span_keys
     rows = len(pos)
     # the merge reads every partition of every (row, kv head)
@@ -61,7 +62,7 @@ def model(case, iters, workspace_floats):
             assert 1 <= np_ <= LONG_PAGES
             assert slot * kept_pages + p0 + np_ - 1 < table.size  # the table rows copied to LDS
             stab = table[slot * kept_pages + p0: slot * kept_pages + p0 + np_].astype(np.int64)
-            for wave in range(LONG_WAVES):
+            for wave in range(waves):
                 w0 = g0 + wave * 32 * iters
                 kb = w0 + 16 * np.arange(2 * iters)  # every block the prefetch loop loads
                 kbc = np.minimum(kb, p_) & ~15
@@ -86,11 +87,13 @@ def test_attend_long_accesses_in_bounds_at_every_iteration_count():
     query = lib.tessera_hip_attend_rows_workspace(C.byref(a)) // 4
     # the library's own split
     model(case, library_split_iters(span), query)
-    # every pinned iteration count, with a workspace sized for that count's partitions
-    for iters in range(1, 33):
-        parts = (span + LONG_WAVES * 32 * iters - 1) // (LONG_WAVES * 32 * iters)
-        need = 32 * case["kv_heads"] * parts * (case["heads"] // case["kv_heads"]) * G_STRIDE
-        assert model(case, iters, need) == parts
+    # every pinned iteration count, with a workspace sized for that count's partitions,
+    # for groups of 2 waves and of 8
+    for waves in (LONG_WAVES, 8):
+        for iters in range(1, 33):
+            parts = (span + waves * 32 * iters - 1) // (waves * 32 * iters)
+            need = 32 * case["kv_heads"] * parts * (case["heads"] // case["kv_heads"]) * G_STRIDE
+            assert model(case, iters, need, waves) == parts
 
 
 def test_model_catches_an_overrun():
