@@ -112,13 +112,15 @@ def test_workspace_sizes():
     r.max_position = 150
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 0  # one group per (row, kv head)
     r.max_position = 8191
-    # long context: attend_rows streams 8 waves x 8 iterations x 32 keys per group (4
+    # long context: attend_rows streams 2 waves x 8 iterations x 32 keys per group (16
     # partitions of (max, sum, 128 acc) per (row, kv head, head)), but the fused
     # attend_step splits the same span into groups of 8 waves x 32 keys (32
     # partitions); the one size covers both
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 32 * 2 * 130 * 4
-    r.rows, r.max_position = 1, 2999  # test_attend_step_fused's ctx 3000: 6 and 12 partitions
-    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 1 * 8 * 12 * 2 * 130 * 4
+    # test_attend_step_fused's ctx 3000: attend_rows 2 waves x 2 iterations x 32 keys
+    # (24 partitions), attend_step 12
+    r.rows, r.max_position = 1, 2999
+    assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 1 * 8 * 24 * 2 * 130 * 4
     r.rows = 32
     r.max_position = 2047  # the short-context kernel: 8 waves x 32 keys, 8 partitions
     assert lib.tessera_hip_attend_rows_workspace(C.byref(r)) == 32 * 8 * 8 * 2 * 130 * 4
