@@ -241,7 +241,7 @@ size_t tessera_hip_attend_rows_workspace(const ts_rows_args *a);
  * fixed device array of tessera_hip_attend_rows_noalloc_limit() bytes (16 MiB; one
  * copy per GPU, held until the process ends). a->workspace is ignored. Launches whose
  * partials would pass the limit (rows * kv_heads * partitions * heads/kv_heads * 520
- * bytes; e.g. 32 rows at 8192 keys need 8.5 MB) fail with TS_ERR_WORKSPACE. Calls
+ * bytes; e.g. 32 rows at 8192 keys, 16 partitions, need 4.3 MB) fail with TS_ERR_WORKSPACE. Calls
  * on one GPU share the array: calls that overlap in time on that GPU (different
  * streams) race; stream-ordered calls do not.
  * No counterpart in the reference: for callers that cannot allocate (code under HIP
