@@ -172,7 +172,8 @@ TS_DEV bool spin(Ctx &c, uint32_t &it, uint64_t &t0) {
             return false;
         }
     }
-    __builtin_amdgcn_s_sleep(1);
+    // No sleep between polls: C1 2437 against 2412 tok/s with s_sleep 1 (longer sleeps
+    // measured slower still).
     return true;
 }
 
